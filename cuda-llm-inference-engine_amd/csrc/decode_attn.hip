@@ -1,0 +1,285 @@
+// decode_attn.hip — split-K paged decode attention for gfx950.
+//
+// Computes what the reference's K13 computes (kernels/decode/13_decode_attn.cuh
+// :30-189 and 13_decode_attn.cu:10-109): for every sequence b and query head h,
+// softmax(q . K^T / sqrt(d)) V over the sequence's first context_lens[b] cached
+// tokens, gathered through the block table, with the work split over KV blocks
+// (pass 1 writes per-split partials (o, m, l); pass 2 merges them).  The split
+// plan is the caller's (the reference rule by default, see capi.cpp).
+//
+// MI355X layout of pass 1 (grid = splits x H_kv x B, 256 threads):
+//   * one workgroup per (b, kv head, split) serves all G = H_q/H_kv query heads
+//     of that KV head, so each K/V byte is read from HBM once (the reference
+//     launches one block per query head and re-reads KV G times);
+//   * the four waves take 16-token chunks of the split round-robin; inside a
+//     chunk each 16-lane DPP row owns one token per step and each lane one
+//     d/16-element slice of it, so a row reads the token's whole K (or V)
+//     vector as one contiguous 256/512-byte run with 16-byte loads;
+//   * q . k is reduced over the row with four DPP rotations; the chunk max
+//     is shared across the wave with two cross-row shuffles, so a wave keeps
+//     one running max per head and rescales once per 16 tokens, not per token;
+//   * scores are pre-multiplied by log2(e)/sqrt(d), so the softmax uses the
+//     hardware exp2; partials store m in that base-2 domain;
+//   * every split writes its slot, empty ones as (o=0, m=-inf, l=0), so the
+//     merge never reads stale workspace (the reference skips the write).
+// Pass 2 (one wave per (b, query head)) merges the splits with l > 0.
+#include <cmath>
+
+#include "device_util.h"
+#include "ie_internal.h"
+
+namespace ie {
+namespace {
+
+template <int EPL>
+__device__ __forceinline__ void load_slice(const float* __restrict__ p, float (&out)[EPL]) {
+#pragma unroll
+    for (int i = 0; i < EPL / 4; ++i) {
+        const float4 v = reinterpret_cast<const float4*>(p)[i];
+        out[4 * i + 0] = v.x;
+        out[4 * i + 1] = v.y;
+        out[4 * i + 2] = v.z;
+        out[4 * i + 3] = v.w;
+    }
+}
+
+template <int EPL>
+__device__ __forceinline__ void load_slice(const uint16_t* __restrict__ p, float (&out)[EPL]) {
+    if constexpr (EPL == 8) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[2 * i + 0] = __builtin_bit_cast(float, w[i] << 16);
+            out[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+        }
+    } else {
+        static_assert(EPL == 4, "slice width");
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            out[2 * i + 0] = __builtin_bit_cast(float, w[i] << 16);
+            out[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+        }
+    }
+}
+
+template <int D, int G, typename KV>
+__global__ __launch_bounds__(256) void decode_attn_split_kernel(
+    const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
+    const int* __restrict__ block_table, const int* __restrict__ context_lens, int H_q,
+    int H_kv, int block_size, int nbps, int num_splits, int blocks_per_split, float qscale,
+    float* __restrict__ ws) {
+    constexpr int EPL = D / 16;
+    constexpr int TPS = 4;  // tokens per lane row per chunk (4 rows x 4 = 16)
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane >> 4, li = lane & 15;
+
+    const int ctx = context_lens[b];
+    const long long span = (long long)blocks_per_split * block_size;
+    const long long t0l = (long long)split * span;
+    // Never walk past the table row, even if context_lens[b] breaks the
+    // caller contract context_lens[b] <= max_context_len.
+    const long long lim = min((long long)ctx, (long long)nbps * block_size);
+    const int tok0 = (int)min(t0l, lim);
+    const int tok1 = (int)min(t0l + span, lim);
+
+    float q[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        load_slice<EPL>(Q + ((size_t)b * H_q + (size_t)kvh * G + g) * D + li * EPL, q[g]);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) q[g][e] *= qscale;
+    }
+
+    float m[G], l[G], o[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
+    }
+
+    const int* bt = block_table + (size_t)b * nbps;
+    const size_t tok_stride = (size_t)H_kv * D;
+    const KV* kbase = kcache + (size_t)kvh * D + li * EPL;
+    const KV* vbase = vcache + (size_t)kvh * D + li * EPL;
+
+    for (int c0 = tok0 + wave * 16; c0 < tok1; c0 += 64) {
+        float kk[TPS][EPL], vv[TPS][EPL];
+        bool valid[TPS];
+#pragma unroll
+        for (int j = 0; j < TPS; ++j) {
+            const int pos = c0 + TPS * j + grp;
+            valid[j] = pos < tok1;
+            if (valid[j]) {
+                const int blk = pos / block_size;
+                const int off = pos - blk * block_size;
+                const size_t row = (size_t)bt[blk] * block_size + off;
+                load_slice<EPL>(kbase + row * tok_stride, kk[j]);
+                load_slice<EPL>(vbase + row * tok_stride, vv[j]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) kk[j][e] = vv[j][e] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float s[TPS];
+#pragma unroll
+            for (int j = 0; j < TPS; ++j) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) dot = fmaf(q[g][e], kk[j][e], dot);
+                dot = row16_sum(dot);
+                s[j] = valid[j] ? dot : -INFINITY;
+            }
+            float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+            cm = fmaxf(cm, xor16(cm));
+            cm = fmaxf(cm, xor32(cm));
+            const float mn = fmaxf(m[g], cm);
+            const float alpha = exp2f(m[g] - mn);
+            float p[TPS], psum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < TPS; ++j) {
+                p[j] = exp2f(s[j] - mn);
+                psum += p[j];
+            }
+            l[g] = fmaf(l[g], alpha, psum);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                float acc = o[g][e] * alpha;
+#pragma unroll
+                for (int j = 0; j < TPS; ++j) acc = fmaf(p[j], vv[j][e], acc);
+                o[g][e] = acc;
+            }
+            m[g] = mn;
+        }
+    }
+
+    // The four lane rows share the wave's running max: plain sums merge them.
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        l[g] += xor16(l[g]);
+        l[g] += xor32(l[g]);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            o[g][e] += xor16(o[g][e]);
+            o[g][e] += xor32(o[g][e]);
+        }
+    }
+
+    __shared__ float sm_m[4][G], sm_l[4][G];
+    __shared__ float sm_o[4][G][D];
+    if (grp == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) sm_o[wave][g][li * EPL + e] = o[g][e];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            sm_m[wave][g] = m[g];
+            sm_l[wave][g] = l[g];
+        }
+    }
+    __syncthreads();
+
+    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+        const int g = idx / D, dd = idx - (idx / D) * D;
+        float mx = fmaxf(fmaxf(sm_m[0][g], sm_m[1][g]), fmaxf(sm_m[2][g], sm_m[3][g]));
+        float ov = 0.0f, lv = 0.0f;
+        if (mx != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float f = exp2f(sm_m[w][g] - mx);
+                ov = fmaf(sm_o[w][g][dd], f, ov);
+                lv = fmaf(sm_l[w][g], f, lv);
+            }
+        }
+        float* dst = ws + (((size_t)b * H_q + (size_t)kvh * G + g) * num_splits + split) * (D + 2);
+        dst[dd] = ov;
+        if (dd == 0) {
+            dst[D] = mx;
+            dst[D + 1] = lv;
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_attn_merge_kernel(int BH, int num_splits,
+                                                                const float* __restrict__ ws,
+                                                                float* __restrict__ O) {
+    constexpr int PER = D / 64;
+    const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (bh >= BH) return;
+    const int lane = threadIdx.x & 63;
+    const float* w = ws + (size_t)bh * num_splits * (D + 2);
+    float mx = -INFINITY;
+    for (int s = 0; s < num_splits; ++s) {
+        const float* p = w + (size_t)s * (D + 2);
+        if (p[D + 1] > 0.0f) mx = fmaxf(mx, p[D]);
+    }
+    float o[PER], l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) o[i] = 0.0f;
+    for (int s = 0; s < num_splits; ++s) {
+        const float* p = w + (size_t)s * (D + 2);
+        const float ls = p[D + 1];
+        if (ls > 0.0f) {
+            const float f = exp2f(p[D] - mx);
+            l = fmaf(ls, f, l);
+#pragma unroll
+            for (int i = 0; i < PER; ++i) o[i] = fmaf(p[lane + 64 * i], f, o[i]);
+        }
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) O[(size_t)bh * D + lane + 64 * i] = o[i] * inv;
+}
+
+template <int D, int G, typename KV>
+void launch_split(const DecodeArgs& a, hipStream_t s) {
+    const float qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+    const dim3 grid(a.num_splits, a.H_kv, a.B);
+    decode_attn_split_kernel<D, G, KV><<<grid, 256, 0, s>>>(
+        a.Q, static_cast<const KV*>(a.k_cache), static_cast<const KV*>(a.v_cache),
+        a.block_table, a.context_lens, a.H_q, a.H_kv, a.block_size, a.num_blocks_per_seq,
+        a.num_splits, a.blocks_per_split, qscale, a.workspace);
+}
+
+template <int D, typename KV>
+void launch_g(const DecodeArgs& a, hipStream_t s) {
+    switch (a.H_q / a.H_kv) {
+        case 1: launch_split<D, 1, KV>(a, s); break;
+        case 2: launch_split<D, 2, KV>(a, s); break;
+        case 4: launch_split<D, 4, KV>(a, s); break;
+        default: launch_split<D, 8, KV>(a, s); break;
+    }
+}
+
+template <int D>
+void launch_d(const DecodeArgs& a, hipStream_t s) {
+    if (a.kv_dtype == IE_KV_BF16)
+        launch_g<D, uint16_t>(a, s);
+    else
+        launch_g<D, float>(a, s);
+    const int BH = a.B * a.H_q;
+    decode_attn_merge_kernel<D><<<(BH + 3) / 4, 256, 0, s>>>(BH, a.num_splits, a.workspace, a.O);
+}
+
+}  // namespace
+
+void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
+    if (a.B == 0) return;
+    if (a.d == 64)
+        launch_d<64>(a, s);
+    else
+        launch_d<128>(a, s);
+}
+
+}  // namespace ie

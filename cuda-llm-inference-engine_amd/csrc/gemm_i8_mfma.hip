@@ -1,0 +1,169 @@
+// gemm_i8_mfma.hip — INT8 GEMM on the gfx950 i8 matrix cores.
+//
+// Same result as the reference's K14 kernel (kernels/quantization/
+// 14_int8_gemm.cu:65-170): exact int32 sum over K of int8 products, then the
+// dequant epilogue.  The reference uses __dp4a with a 64x64 tile and a 4x4
+// register tile; here the sum runs on v_mfma_i32_32x32x32_i8 (32x32 outputs,
+// 32 K-bytes per instruction) with LDS-staged int8 tiles.
+//
+// Tiling: a 256-thread workgroup (4 waves, 2x2) computes a 128x128 tile of C;
+// each wave a 64x64 sub-tile as 2x2 MFMA blocks (64 int32 accumulators/lane).
+// K advances 64 bytes per step; the next step's A/B tiles are fetched from
+// global memory into registers while the current step runs on the matrix
+// cores, then written to the other half of a double-buffered LDS (one barrier
+// per step).  LDS rows are padded from 64 to 80 bytes, which makes both the
+// 16-byte writes and the 16-byte MFMA-operand reads bank-conflict free.
+//
+// MFMA operand convention: lane l supplies row (l % 32) of A and column
+// (l % 32) of B, each with 16 K-bytes; A and B take the same K-bytes from the
+// same lane, so the product is the full K-sum whatever order the hardware
+// adds them in.  Accumulator v of lane l holds C[8*(v/4) + 4*(l/32) + v%4]
+// [l % 32] of the 32x32 block.
+#include "device_util.h"
+#include "epilogue.h"
+#include "ie_internal.h"
+
+namespace ie {
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int LDS_STRIDE = BK + 16;           // bytes per LDS row
+constexpr int TILE_BYTES = BM * LDS_STRIDE;   // one operand, one stage
+
+struct TileRegs {
+    i32x4 a[2];
+    i32x4 b[2];
+};
+
+__device__ __forceinline__ void load_tile(TileRegs& r, const int8_t* __restrict__ A,
+                                          const int8_t* __restrict__ BT, int M, int N,
+                                          int K, int m0, int n0, int k0) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = (t >> 2) + h * 64;
+        const int kc = k0 + (t & 3) * 16;
+        const i32x4 zero = {0, 0, 0, 0};
+        const int gm = m0 + row, gn = n0 + row;
+        r.a[h] = (gm < M && kc < K)
+                     ? *reinterpret_cast<const i32x4*>(A + (size_t)gm * K + kc)
+                     : zero;
+        r.b[h] = (gn < N && kc < K)
+                     ? *reinterpret_cast<const i32x4*>(BT + (size_t)gn * K + kc)
+                     : zero;
+    }
+}
+
+__device__ __forceinline__ void store_tile(const TileRegs& r, int8_t* As, int8_t* Bs) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = (t >> 2) + h * 64;
+        const int off = row * LDS_STRIDE + (t & 3) * 16;
+        *reinterpret_cast<i32x4*>(As + off) = r.a[h];
+        *reinterpret_cast<i32x4*>(Bs + off) = r.b[h];
+    }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_i8_mfma_kernel(
+    int M, int N, int K, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
+    const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
+    const float* residual, void* C) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[2 * 2 * TILE_BYTES];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    i32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+    const int nk = (K + BK - 1) / BK;
+    TileRegs r;
+    load_tile(r, A, BT, M, N, K, m0, n0, 0);
+    store_tile(r, lds, lds + TILE_BYTES);
+    __syncthreads();
+
+    const int lrow = lane & 31;
+    const int lk = (lane >> 5) * 16;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const int8_t* As = lds + cur * 2 * TILE_BYTES;
+        const int8_t* Bs = As + TILE_BYTES;
+        if (kt + 1 < nk) load_tile(r, A, BT, M, N, K, m0, n0, (kt + 1) * BK);
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            i32x4 af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                af[i] = *reinterpret_cast<const i32x4*>(
+                    As + (wm * 64 + i * 32 + lrow) * LDS_STRIDE + ks * 32 + lk);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                bf[j] = *reinterpret_cast<const i32x4*>(
+                    Bs + (wn * 64 + j * 32 + lrow) * LDS_STRIDE + ks * 32 + lk);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j],
+                                                                     0, 0, 0);
+        }
+        if (kt + 1 < nk) {
+            int8_t* Ns = lds + (cur ^ 1) * 2 * TILE_BYTES;
+            store_tile(r, Ns, Ns + TILE_BYTES);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (n >= N) continue;
+            float sb = 0.0f;
+            if constexpr (EPI != IE_EPI_I32) sb = sB[n];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (m < M) {
+                    float sa = 0.0f;
+                    if constexpr (EPI != IE_EPI_I32) sa = sA[m];
+                    store_epilogue<EPI>(C, (size_t)m * N + n, acc[i][j][v], sa, sb, bias,
+                                        residual, n);
+                }
+            }
+        }
+    }
+}
+
+template <int EPI>
+struct MfmaLaunch {
+    static void run(const GemmArgs& a, hipStream_t s) {
+        const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+        gemm_i8_mfma_kernel<EPI><<<grid, 256, 0, s>>>(
+            a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A),
+            reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
+    }
+};
+
+}  // namespace
+
+void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s) {
+    if (a.M == 0 || a.N == 0) return;
+    const bool vec = (a.K % 16) == 0 && ((uintptr_t)a.A % 16) == 0 && ((uintptr_t)a.BT % 16) == 0;
+    if (!vec) {
+        launch_gemm_i8_generic(a, s);
+        return;
+    }
+    dispatch_epilogue<MfmaLaunch>(a.epi, a, s);
+}
+
+}  // namespace ie

@@ -1,0 +1,84 @@
+// ie_internal.h — shared declarations between the C ABI (capi.cpp) and the
+// kernel translation units.  Launchers assume their arguments were validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "ie_amd.h"
+
+namespace ie {
+
+// Records a failure message for ie_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps a HIP error after a launch to IE_ERR_HIP with a message.
+int check_launch(const char* what);
+
+// ---- quantizer (quant.hip) ----
+void launch_quantize(int rows, int cols, const float* in, int32_t* packed,
+                     float* scales, hipStream_t s);
+
+// ---- INT8 GEMM ----
+struct GemmArgs {
+    int M, N, K;
+    const int32_t* A;
+    const int32_t* BT;
+    const float* sA;
+    const float* sB;
+    const float* bias;
+    const float* residual;
+    void* C;
+    int epi;
+};
+// dot4 GEMV for small M (gemv_i8.hip); M in [1, 16].
+void launch_gemv_i8(const GemmArgs& a, hipStream_t s);
+// MFMA tile GEMM (gemm_i8_mfma.hip); any M.
+void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s);
+// One thread per output; any K % 4 == 0 and any alignment (gemv_i8.hip).
+void launch_gemm_i8_generic(const GemmArgs& a, hipStream_t s);
+constexpr int kGemvMaxM = 16;
+
+// ---- decode attention (decode_attn.hip) ----
+struct DecodeArgs {
+    int B, H_q, H_kv, d;
+    const float* Q;
+    const void* k_cache;
+    const void* v_cache;
+    int kv_dtype;
+    const int* block_table;
+    const int* context_lens;
+    int block_size;
+    int num_blocks_per_seq;
+    int num_splits;        // plan: splits per (b, head)
+    int blocks_per_split;  // plan: KV blocks per split
+    float* O;
+    float* workspace;      // [B, H_q, num_splits, d + 2]
+};
+void launch_decode_attn(const DecodeArgs& a, hipStream_t s);
+
+// ---- KV cache (kv_cache.hip) ----
+void launch_kv_write(const float* K, const float* V, void* kc, void* vc,
+                     int kv_dtype, const int* bt, int seq_len, int start_pos,
+                     int H, int dh, int bs, hipStream_t s);
+void launch_kv_append_batch(int B, const float* K, const float* V, void* kc,
+                            void* vc, int kv_dtype, const int* bt, int nbps,
+                            const int* positions, int H, int dh, int bs,
+                            hipStream_t s);
+
+// ---- support ops (support.hip) ----
+void launch_layernorm(int rows, int cols, const float* x, const float* g,
+                      const float* b, float* out, float eps, hipStream_t s);
+void launch_embedding(const int* ids, int seq_len, int start_pos, int d,
+                      const float* wte, const float* wpe, float* out,
+                      hipStream_t s);
+void launch_embedding_batch(int B, const int* ids, const int* positions, int d,
+                            const float* wte, const float* wpe, float* out,
+                            hipStream_t s);
+void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits,
+                       int d, int V, hipStream_t s);
+void launch_argmax(int rows, const float* logits, int n, int* out,
+                   hipStream_t s);
+
+}  // namespace ie

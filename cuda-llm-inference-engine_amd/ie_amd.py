@@ -1,0 +1,215 @@
+"""ctypes binding of libie_amd.so (include/ie_amd.h) for tests and benchmarks.
+
+The product is the C ABI; this module only marshals torch device tensors into
+it.  It never falls back to anything: if the HIP library is missing or a call
+is rejected, it raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libie_amd.so")
+
+IE_OK, IE_ERR_INVALID, IE_ERR_UNSUPPORTED, IE_ERR_WORKSPACE, IE_ERR_HIP = range(5)
+EPI_PLAIN, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESIDUAL, EPI_I32 = range(5)
+PATH_AUTO, PATH_GEMV, PATH_MFMA = range(3)
+KV_F32, KV_BF16 = 0, 1
+DA_REF_MAX_SPLITS = 16
+DA_MAX_SPLITS = 256
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_Z = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/ie_amd.h one to one.
+SIGNATURES = {
+    "ie_last_error": (ctypes.c_char_p, []),
+    "ie_version": (_I, []),
+    "ie_init": (_I, []),
+    "ie_quantize_fp32_to_int8": (_I, [_I, _I, _P, _P, _P, _P]),
+    "ie_int8_gemm": (_I, [_I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
+    "ie_int8_gemm_ex": (_I, [_I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _I, _P]),
+    "ie_decode_num_splits": (_I, [_I, _I, _I]),
+    "ie_decode_attn_workspace_bytes": (_Z, [_I, _I, _I, _I]),
+    "ie_decode_attn": (_I, [_I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P, _P, _Z, _I, _P]),
+    "ie_kv_cache_write": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P]),
+    "ie_kv_cache_append_batch": (_I, [_I, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _P]),
+    "ie_layernorm": (_I, [_I, _I, _P, _P, _P, _P, _F, _P]),
+    "ie_embedding": (_I, [_P, _I, _I, _I, _P, _P, _P, _P]),
+    "ie_embedding_batch": (_I, [_I, _P, _P, _I, _P, _P, _P, _P]),
+    "ie_vocab_proj": (_I, [_I, _P, _P, _P, _I, _I, _P]),
+    "ie_argmax": (_I, [_I, _P, _I, _P, _P]),
+}
+
+
+class IeError(RuntimeError):
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn} failed with status {status}: {msg}")
+        self.status = status
+        self.msg = msg
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads libie_amd.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        # torch ships its own libamdhip64 (file libamdhip64.so, soname
+        # libamdhip64.so.7).  Loading torch first makes the dynamic loader bind
+        # our libamdhip64.so.7 dependency to that copy; the other order maps
+        # two HIP/HSA runtimes into the process and the second sees no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                "(make -C cuda-llm-inference-engine_amd)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().ie_last_error().decode()
+
+
+def call(name: str, *args) -> int:
+    """Calls an ie_* entry point and returns its status without raising."""
+    return getattr(load(), name)(*args)
+
+
+def check(name: str, *args) -> None:
+    st = call(name, *args)
+    if st != IE_OK:
+        raise IeError(name, st, last_error())
+
+
+# ---------------------------------------------------------------- torch glue
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def quantize(x, out_packed=None, out_scales=None, stream=None):
+    """x: [rows, cols] fp32 cuda -> (packed int32 [rows, cols/4], scales [rows])."""
+    import torch
+
+    rows, cols = x.shape
+    packed = out_packed if out_packed is not None else torch.empty(
+        (rows, cols // 4), dtype=torch.int32, device=x.device)
+    scales = out_scales if out_scales is not None else torch.empty(
+        rows, dtype=torch.float32, device=x.device)
+    check("ie_quantize_fp32_to_int8", rows, cols, _ptr(x), _ptr(packed), _ptr(scales), _stream(stream))
+    return packed, scales
+
+
+def int8_gemm(A_packed, BT_packed, sA=None, sB=None, epilogue=EPI_PLAIN, bias=None,
+              residual=None, out=None, path=PATH_AUTO, stream=None):
+    """Returns C [M, N] (fp32, or int32 for EPI_I32)."""
+    import torch
+
+    M, K4 = A_packed.shape
+    N = BT_packed.shape[0]
+    if out is None:
+        dt = torch.int32 if epilogue == EPI_I32 else torch.float32
+        out = torch.empty((M, N), dtype=dt, device=A_packed.device)
+    check("ie_int8_gemm_ex", M, N, 4 * K4, _ptr(A_packed), _ptr(BT_packed), _ptr(sA), _ptr(sB),
+          epilogue, _ptr(bias), _ptr(residual), _ptr(out), path, _stream(stream))
+    return out
+
+
+def num_splits(max_ctx: int, block_size: int, splits: int = 0) -> int:
+    return call("ie_decode_num_splits", max_ctx, block_size, splits)
+
+
+def workspace_bytes(B: int, H_q: int, d: int, splits: int) -> int:
+    return call("ie_decode_attn_workspace_bytes", B, H_q, d, splits)
+
+
+def decode_attn(Q, k_cache, v_cache, block_table, context_lens, max_ctx, block_size, H_kv,
+                kv_dtype=KV_F32, splits=0, out=None, workspace=None, stream=None):
+    """Q [B, H_q, d] fp32; caches [P, bs, H_kv, d]; returns O [B, H_q, d]."""
+    import torch
+
+    B, H_q, d = Q.shape
+    nbps = block_table.shape[1]
+    S = num_splits(max_ctx, block_size, splits)
+    need = workspace_bytes(B, H_q, d, S)
+    if workspace is None:
+        workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=Q.device)
+    if out is None:
+        out = torch.empty_like(Q)
+    check("ie_decode_attn", B, H_q, H_kv, d, _ptr(Q), _ptr(k_cache), _ptr(v_cache), kv_dtype,
+          _ptr(block_table), _ptr(context_lens), max_ctx, block_size, nbps, _ptr(out),
+          _ptr(workspace), workspace.numel() * 4, splits, _stream(stream))
+    return out
+
+
+def kv_cache_write(K, V, k_cache, v_cache, block_table, start_pos, block_size,
+                   kv_dtype=KV_F32, stream=None):
+    seq, H, dh = K.shape
+    check("ie_kv_cache_write", _ptr(K), _ptr(V), _ptr(k_cache), _ptr(v_cache), kv_dtype,
+          _ptr(block_table), seq, start_pos, H, dh, block_size, _stream(stream))
+
+
+def kv_cache_append_batch(K, V, k_cache, v_cache, block_table, positions, block_size,
+                          kv_dtype=KV_F32, stream=None):
+    B, H, dh = K.shape
+    check("ie_kv_cache_append_batch", B, _ptr(K), _ptr(V), _ptr(k_cache), _ptr(v_cache), kv_dtype,
+          _ptr(block_table), block_table.shape[1], _ptr(positions), H, dh, block_size,
+          _stream(stream))
+
+
+def layernorm(x, gamma, beta, out=None, eps=1e-5, stream=None):
+    import torch
+
+    rows, cols = x.shape
+    out = out if out is not None else torch.empty_like(x)
+    check("ie_layernorm", rows, cols, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(out), eps, _stream(stream))
+    return out
+
+
+def embedding(ids, start_pos, wte, wpe, out=None, stream=None):
+    import torch
+
+    seq = ids.shape[0]
+    d = wte.shape[1]
+    out = out if out is not None else torch.empty((seq, d), dtype=torch.float32, device=wte.device)
+    check("ie_embedding", _ptr(ids), seq, start_pos, d, _ptr(wte), _ptr(wpe), _ptr(out), _stream(stream))
+    return out
+
+
+def vocab_proj(h, wte, out=None, stream=None):
+    import torch
+
+    rows, d = h.shape
+    V = wte.shape[0]
+    out = out if out is not None else torch.empty((rows, V), dtype=torch.float32, device=h.device)
+    check("ie_vocab_proj", rows, _ptr(h), _ptr(wte), _ptr(out), d, V, _stream(stream))
+    return out
+
+
+def argmax(logits, out=None, stream=None):
+    import torch
+
+    rows, n = logits.shape
+    out = out if out is not None else torch.empty(rows, dtype=torch.int32, device=logits.device)
+    check("ie_argmax", rows, _ptr(logits), n, _ptr(out), _stream(stream))
+    return out

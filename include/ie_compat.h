@@ -1,0 +1,62 @@
+/*
+ * ie_compat.h — the reference's own C++ launch signatures, unchanged, so code
+ * written against the reference (its engine, tests and benchmarks) links
+ * against libie_amd.so without edits.
+ *
+ *   kernels/quantization/14_int8_gemm.cuh:20-64   quantizer, INT8 GEMM, epilogues
+ *   kernels/decode/13_decode_attn.cuh:12,192-199   DA_MAX_SPLITS, run_decode_attn
+ *   kernels/layernorm/15_layernorm_residual.cuh    run_layernorm
+ *   kernels/layernorm/15_embed.cuh                 run_embedding
+ *
+ * As in the reference: void return, caller-owned device pointers, the null
+ * stream, asynchronous.  Unlike the reference, invalid arguments never reach a
+ * kernel: the call prints the reason to stderr, leaves the outputs untouched
+ * and records it for ie_last_error().  For stream selection, status codes,
+ * bf16 KV or more than DA_MAX_SPLITS splits, use ie_amd.h.
+ */
+#ifndef IE_COMPAT_H
+#define IE_COMPAT_H
+
+#include <cstdint>
+
+#include "ie_amd.h"
+
+/* Workspace sizing used by callers of run_decode_attn:
+ * [B, H_q, DA_MAX_SPLITS, d + 2] floats (src/gpt2_engine.cu:156). */
+#define DA_MAX_SPLITS 16
+
+void run_quantize_fp32_to_int8(int rows, int cols, const float* input,
+                               int32_t* output_packed, float* scales);
+
+void run_int8_gemm(int M, int N, int K, const int32_t* A_packed,
+                   const int32_t* BT_packed, const float* scale_A,
+                   const float* scale_B, float* C);
+
+enum class I8Epilogue { Plain, BiasOnly, BiasGELU, BiasResidual };
+
+void run_int8_gemm_bias(int M, int N, int K, const int32_t* A_packed,
+                        const int32_t* BT_packed, const float* scale_A,
+                        const float* scale_B, const float* bias, float* C);
+
+void run_int8_gemm_bias_gelu(int M, int N, int K, const int32_t* A_packed,
+                             const int32_t* BT_packed, const float* scale_A,
+                             const float* scale_B, const float* bias, float* C);
+
+void run_int8_gemm_bias_residual(int M, int N, int K, const int32_t* A_packed,
+                                 const int32_t* BT_packed, const float* scale_A,
+                                 const float* scale_B, const float* bias,
+                                 const float* residual, float* C);
+
+void run_decode_attn(int B, int H_q, int H_kv, int d, const float* Q,
+                     const float* k_cache, const float* v_cache,
+                     const int* block_table, const int* context_lens,
+                     int max_context_len, int block_size,
+                     int num_blocks_per_seq, float* O, float* workspace);
+
+void run_layernorm(int rows, int cols, const float* x, const float* gamma,
+                   const float* beta, float* out, float eps = 1e-5f);
+
+void run_embedding(const int* token_ids, int seq_len, int start_pos,
+                   int d_model, const float* wte, const float* wpe, float* out);
+
+#endif

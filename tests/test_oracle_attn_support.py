@@ -1,0 +1,197 @@
+"""Pins the CPU oracle's decode attention, KV write and support ops (CPU only).
+
+Decode attention is checked against textbook softmax attention evaluated by
+numpy (and torch's scaled_dot_product_attention) in fp64 on the logically
+gathered K/V - the reference's intended semantics, tests/test_paged_attention.cu
+:138-179 generalised to one query token - plus closed forms (ctx = 1 gives V0,
+constant V rows give that row) and invariances (block placement, split count).
+"""
+import numpy as np
+import pytest
+
+from conftest import bf16_bits, bf16_to_f32, make_paged_cache, rng
+
+
+def textbook(Q, Ks, Vs, H_kv):
+    B, H_q, d = Q.shape
+    G = H_q // H_kv
+    scale = np.float64(np.float32(1.0) / np.sqrt(np.float32(d)))
+    O = np.zeros((B, H_q, d), dtype=np.float64)
+    for b in range(B):
+        for h in range(H_q):
+            k = Ks[b][:, h // G, :].astype(np.float64)
+            v = Vs[b][:, h // G, :].astype(np.float64)
+            if k.shape[0] == 0:
+                continue
+            s = k @ Q[b, h].astype(np.float64) * scale
+            p = np.exp(s - s.max())
+            O[b, h] = (p / p.sum()) @ v
+    return O
+
+
+def glibc_reference_case(orc, B, H_q, H_kv, ctx, d, bs):
+    """tests/test_decode_attention.cu:48-98 inputs and identity block table."""
+    g = orc.GlibcRand(42)
+    Q = g.uniform(B * H_q * d).reshape(B, H_q, d)
+    Kf, Vf = g.uniform_pair(B * H_kv * ctx * d)
+    Kf = Kf.reshape(B, H_kv, ctx, d)
+    Vf = Vf.reshape(B, H_kv, ctx, d)
+    nbps = (ctx + bs - 1) // bs
+    kc = np.zeros((B * nbps, bs, H_kv, d), dtype=np.float32)
+    vc = np.zeros_like(kc)
+    table = np.arange(B * nbps, dtype=np.int32).reshape(B, nbps)
+    for b in range(B):
+        for t in range(ctx):
+            kc[b * nbps + t // bs, t % bs] = Kf[b, :, t]
+            vc[b * nbps + t // bs, t % bs] = Vf[b, :, t]
+    Ks = [np.ascontiguousarray(Kf[b].transpose(1, 0, 2)) for b in range(B)]
+    Vs = [np.ascontiguousarray(Vf[b].transpose(1, 0, 2)) for b in range(B)]
+    lens = np.full(B, ctx, dtype=np.int32)
+    return Q, kc, vc, table, lens, Ks, Vs
+
+
+REF_CASES = [(1, 8, 8, 128, 64, 16), (1, 16, 16, 512, 64, 16), (4, 8, 8, 256, 64, 16),
+             (1, 8, 8, 1024, 64, 16), (1, 16, 4, 256, 64, 16), (8, 32, 8, 1024, 64, 16)]
+
+
+@pytest.mark.parametrize("case", REF_CASES)
+def test_reference_cases_vs_textbook(orc, case):
+    B, H_q, H_kv, ctx, d, bs = case
+    Q, kc, vc, table, lens, Ks, Vs = glibc_reference_case(orc, *case)
+    want = textbook(Q, Ks, Vs, H_kv)
+    got = orc.decode_attn(Q, kc, vc, table, lens, ctx, bs, H_kv)
+    assert np.abs(got - want).max() < 1e-6 * np.abs(want).max() + 1e-7
+    # the fp32 restatement of the reference kernel meets the reference's own
+    # bound (max abs error < 1e-5, tests/test_decode_attention.cu:49)
+    got32 = orc.decode_attn(Q, kc, vc, table, lens, ctx, bs, H_kv, f32=True)
+    assert np.abs(got32 - want).max() < 1e-5
+
+
+@pytest.mark.parametrize("B,H_q,H_kv,d,ctx", [(3, 8, 2, 128, 300), (5, 12, 12, 64, 777), (2, 32, 4, 128, 1030)])
+def test_shuffled_variable_lengths_vs_torch(orc, B, H_q, H_kv, d, ctx):
+    import torch
+
+    r = rng(B * 7 + d)
+    lens = r.integers(ctx // 2, ctx + 1, B)
+    lens[0] = ctx
+    kc, vc, table, Ks, Vs = make_paged_cache(r, B, H_kv, d, lens, 16)
+    Q = r.standard_normal((B, H_q, d)).astype(np.float32)
+    got = orc.decode_attn(Q, kc, vc, table, lens, ctx, 16, H_kv)
+    G = H_q // H_kv
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    for b in range(B):
+        q = torch.from_numpy(Q[b]).double()[:, None, :]                       # [H_q,1,d]
+        k = torch.from_numpy(Ks[b]).double().permute(1, 0, 2).repeat_interleave(G, 0)
+        v = torch.from_numpy(Vs[b]).double().permute(1, 0, 2).repeat_interleave(G, 0)
+        o = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale)[:, 0, :].numpy()
+        # the oracle accumulates in fp64 and rounds its output to fp32
+        assert np.abs(got[b] - o).max() <= 1e-6 * np.abs(o).max()
+
+
+def test_closed_forms(orc):
+    r = rng(5)
+    B, H, d = 2, 4, 64
+    # ctx = 1: softmax over one token is 1, O = V0
+    kc, vc, table, Ks, Vs = make_paged_cache(r, B, H, d, [1, 1], 16)
+    Q = r.standard_normal((B, H, d)).astype(np.float32)
+    got = orc.decode_attn(Q, kc, vc, table, np.array([1, 1]), 1, 16, H)
+    for b in range(B):
+        assert np.array_equal(got[b], Vs[b][0])
+    # constant V rows: O equals that row whatever the scores are
+    row = r.standard_normal((H, d)).astype(np.float32)
+
+    def fill(b, c):
+        return r.standard_normal((c, H, d)).astype(np.float32) * 3, np.broadcast_to(row, (c, H, d)).copy()
+
+    kc, vc, table, Ks, Vs = make_paged_cache(r, B, H, d, [100, 37], 16, fill=fill)
+    got = orc.decode_attn(Q, kc, vc, table, np.array([100, 37]), 100, 16, H)
+    assert np.allclose(got, np.broadcast_to(row, got.shape), rtol=1e-12, atol=1e-12)
+    # empty sequence -> zeros
+    got = orc.decode_attn(Q, kc, vc, table, np.array([0, 37]), 100, 16, H)
+    assert np.all(got[0] == 0) and np.allclose(got[1], row, atol=1e-12)
+
+
+def test_invariances(orc):
+    r = rng(9)
+    B, H_q, H_kv, d, ctx = 3, 8, 2, 128, 700
+    lens = np.array([700, 413, 650])
+    kc, vc, table, Ks, Vs = make_paged_cache(rng(1), B, H_kv, d, lens, 16, shuffle=True)
+    kc2, vc2, table2, _, _ = make_paged_cache(rng(1), B, H_kv, d, lens, 16, shuffle=False)
+    Q = r.standard_normal((B, H_q, d)).astype(np.float32)
+    a = orc.decode_attn(Q, kc, vc, table, lens, ctx, 16, H_kv)
+    b = orc.decode_attn(Q, kc2, vc2, table2, lens, ctx, 16, H_kv)
+    assert np.array_equal(a, b)  # placement of physical blocks is invisible
+    for S in (1, 3, 16, 44):
+        c = orc.decode_attn(Q, kc, vc, table, lens, ctx, 16, H_kv, splits=S)
+        assert np.abs(c - a).max() <= 1e-6 * np.abs(a).max()
+    # identical queries across a GQA group give identical outputs
+    Q[:, 1] = Q[:, 0]
+    c = orc.decode_attn(Q, kc, vc, table, lens, ctx, 16, H_kv)
+    assert np.array_equal(c[:, 0], c[:, 1])
+
+
+def test_bf16_cache_is_upcast_fp32(orc):
+    r = rng(21)
+    B, H_q, H_kv, d, lens = 2, 8, 2, 128, np.array([90, 200])
+    kc, vc, table, Ks, Vs = make_paged_cache(r, B, H_kv, d, lens, 16)
+    Q = r.standard_normal((B, H_q, d)).astype(np.float32)
+    kb, vb = bf16_bits(kc), bf16_bits(vc)
+    got = orc.decode_attn(Q, kb, vb, table, lens, 200, 16, H_kv, kv_dtype=1)
+    want = orc.decode_attn(Q, bf16_to_f32(kb), bf16_to_f32(vb), table, lens, 200, 16, H_kv)
+    assert np.array_equal(got, want)
+
+
+def test_split_rule(orc):
+    # 13_decode_attn.cu:63: clamp(ceil(ctx/bs)/4, 1, 16)
+    assert orc.decode_num_splits(1, 16) == 1
+    assert orc.decode_num_splits(128, 16) == 2
+    assert orc.decode_num_splits(1024, 16) == 16
+    assert orc.decode_num_splits(32768, 16) == 16
+    assert orc.decode_num_splits(400, 16) == 6
+
+
+# ---------------------------------------------------------------- KV write
+def test_kv_write_index_map(orc):
+    r = rng(2)
+    P, bs, H, dh = 9, 16, 3, 8
+    kc = np.zeros((P, bs, H, dh), dtype=np.float32)
+    vc = np.zeros_like(kc)
+    table = r.permutation(P).astype(np.int32)
+    seq, start = 20, 13
+    K = r.standard_normal((seq, H, dh)).astype(np.float32)
+    V = r.standard_normal((seq, H, dh)).astype(np.float32)
+    orc.kv_cache_write(K, V, kc, vc, table, start, bs)
+    pos = np.arange(start, start + seq)
+    assert np.array_equal(kc[table[pos // bs], pos % bs], K)
+    assert np.array_equal(vc[table[pos // bs], pos % bs], V)
+    untouched = np.ones((P, bs), bool)
+    untouched[table[pos // bs], pos % bs] = False
+    assert np.all(kc[untouched] == 0)
+
+
+# ---------------------------------------------------------------- support ops
+def test_layernorm_vs_torch(orc):
+    import torch
+
+    r = rng(4)
+    x = (r.standard_normal((5, 768)) * 3 + 1).astype(np.float32)
+    g = r.standard_normal(768).astype(np.float32)
+    b = r.standard_normal(768).astype(np.float32)
+    got = orc.layernorm(x, g, b)
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (768,),
+                                          torch.from_numpy(g).double(), torch.from_numpy(b).double(),
+                                          eps=1e-5).numpy()
+    assert np.abs(got - want).max() < 1e-5
+
+
+def test_embedding_vocab_argmax(orc):
+    r = rng(6)
+    V, d, L = 50, 16, 20
+    wte = r.standard_normal((V, d)).astype(np.float32)
+    wpe = r.standard_normal((L, d)).astype(np.float32)
+    ids = np.array([3, 49, 0], dtype=np.int32)
+    assert np.array_equal(orc.embedding(ids, 5, wte, wpe), wte[ids] + wpe[5:8])
+    h = r.standard_normal(d).astype(np.float32)
+    assert np.allclose(orc.vocab_proj(h, wte), wte.astype(np.float64) @ h, rtol=1e-6, atol=1e-6)
+    logits = np.array([1.0, 3.0, -2.0, 3.0, 0.5], dtype=np.float32)
+    assert orc.argmax(logits) == int(np.argmax(logits)) == 1
