@@ -1,0 +1,345 @@
+#!/usr/bin/env python3
+"""Measures the INT8 decode hot path on one MI355X.
+
+Headline (`value`): INT8 GEMM throughput at M=N=K=8192 (Plain epilogue, int32
+accumulate, fp32 out) in TOP/s, one "step" = one GEMM launch over resident
+inputs.  The same JSON line carries:
+  roofline      the 8192^3 kernel against the dense i8 MFMA peak (5.0 POP/s)
+  gemv          decode-M (1, 4, 16) GEMMs on the GPT-2 weight shapes, the LM
+                head shape and 8192x8192, in GB/s of algorithmic bytes against
+                HBM (8 TB/s), weights rotated through >= 1 GiB of copies so the
+                256 MiB MALL cannot serve them
+  gemm_m512     the GPT-2 shapes at M = 512 (prefill-sized), TOP/s
+  decode_attn   split-K paged decode attention, BASELINE cfg3 (MHA) and cfg4
+                (GQA, ctx 4096/8192/32768, fp32 and bf16 KV), GB/s of
+                algorithmic bytes against HBM
+  cpu_baseline  the C oracle (oracle/liborc.so) on a bounded sample of the
+                8192^3 GEMM, on this host's cores
+Kernel durations come from HIP events on the stream the kernels run on.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "cuda-llm-inference-engine_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, GB/s
+PEAK_I8_TOPS = 5000.0      # MI355X dense int8 MFMA, TOP/s
+METRIC = "INT8 GEMM TOPS & decode-attn GB/s (% peak); GPT-2-124M decode tok/s, 1 GPU"
+ROTATE_BYTES = 1 << 30     # rotate weight/KV copies through >= 1 GiB
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip", default="", help="comma list of gemv,gemm512,attn,cpu,e2e")
+    ap.add_argument("--only-headline", action="store_true")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the current torch stream (where the library launches)."""
+
+    def __init__(self):
+        import torch
+
+        self.s = torch.cuda.Event(enable_timing=True)
+        self.e = torch.cuda.Event(enable_timing=True)
+
+    def __enter__(self):
+        self.s.record()
+        return self
+
+    def __exit__(self, *a):
+        import torch
+
+        self.e.record()
+        torch.cuda.synchronize()
+        self.ms = self.s.elapsed_time(self.e)
+
+
+def graph_time(launch, count, reps=3):
+    """Captures `count` launches (launch(i)) into one HIP graph and returns the
+    mean device time per launch in ms over `reps` replays, so host launch cost
+    does not leave the GPU idle between small kernels."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(min(count, 3)):  # warm up outside capture
+            launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(count):
+            launch(i)
+    g.replay()
+    torch.cuda.synchronize()
+    with Timer() as t:
+        for _ in range(reps):
+            g.replay()
+    return t.ms / (reps * count)
+
+
+def roof(achieved, peak, unit, bound, traffic=None):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def gemm_bytes(M, N, K, bias=False, residual=False):
+    b = M * K + N * K + 4 * M + 4 * N + 4 * M * N
+    return b + (4 * N if bias else 0) + (4 * M * N if residual else 0)
+
+
+# ------------------------------------------------------------------ headline
+def bench_headline(ie, steps, warmup):
+    import torch
+
+    M = N = K = 8192
+    # BASELINE recipe: A, B fp32 ~ N(0,1) from a seed; A quantized per row and
+    # B per column (= per row of B^T) with the library's quantizer (untimed).
+    g = torch.Generator(device="cuda").manual_seed(42)
+    Af = torch.randn((M, K), device="cuda", generator=g)
+    Ap, sA = ie.quantize(Af)
+    del Af
+    BTf = torch.randn((N, K), device="cuda", generator=g)
+    Bp, sB = ie.quantize(BTf)
+    del BTf
+    torch.cuda.empty_cache()
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+
+    def launch():
+        ie.int8_gemm(Ap, Bp, sA, sB, ie.EPI_PLAIN, out=C)
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with Timer() as t:
+        for _ in range(steps):
+            launch()
+    wall = time.perf_counter() - t0
+    ops = 2.0 * M * N * K
+    kern_ms = t.ms / steps
+    return {
+        "ms_per_step": wall * 1e3 / steps,
+        "value": ops / (wall / steps) / 1e12,
+        "kernel_ms": kern_ms,
+        "kernel_tops": ops / (kern_ms * 1e-3) / 1e12,
+        "bytes": gemm_bytes(M, N, K),
+        "inputs": (Ap, Bp, sA, sB),
+    }
+
+
+# ------------------------------------------------------------------ GEMV
+def bench_gemv(ie):
+    import torch
+
+    shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 50257), (8192, 8192)]
+    out = []
+    g = torch.Generator(device="cuda").manual_seed(7)
+    for K, N in shapes:
+        wbytes = N * K
+        R = max(8, -(-ROTATE_BYTES // wbytes))
+        W = torch.randint(-127, 128, (R, N, K), dtype=torch.int8, device="cuda", generator=g)
+        Wp = W.view(torch.int32)
+        sB = torch.rand(N, device="cuda", generator=g) * 0.01
+        bias = torch.randn(N, device="cuda", generator=g)
+        for M in (1, 4, 16):
+            A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=g)
+            Ap = A.view(torch.int32)
+            sA = torch.rand(M, device="cuda", generator=g) * 0.01
+            C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            ms = graph_time(lambda i: ie.int8_gemm(Ap, Wp[i % R], sA, sB, ie.EPI_PLAIN, out=C), R)
+            byts = gemm_bytes(M, N, K)
+            gbs = byts / (ms * 1e-3) / 1e9
+            out.append({"M": M, "K": K, "N": N, "us": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 3)})
+            log(f"gemv M={M} K={K} N={N}: {ms * 1e3:.2f} us {gbs:.0f} GB/s")
+        del W, Wp
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_gemm512(ie):
+    import torch
+
+    out = []
+    g = torch.Generator(device="cuda").manual_seed(8)
+    M = 512
+    for K, N in [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 50257)]:
+        A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
+        B = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
+        sA = torch.rand(M, device="cuda", generator=g)
+        sB = torch.rand(N, device="cuda", generator=g)
+        C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        ms = graph_time(lambda i: ie.int8_gemm(A, B, sA, sB, ie.EPI_PLAIN, out=C), 20)
+        tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        out.append({"M": M, "K": K, "N": N, "us": round(ms * 1e3, 2), "TOPs": round(tops, 1)})
+        log(f"gemm M=512 K={K} N={N}: {ms * 1e3:.2f} us {tops:.1f} TOP/s")
+    return out
+
+
+# ------------------------------------------------------------------ attention
+def attn_case(ie, B, H_q, H_kv, d, ctx, kv_bf16, uniform, seed):
+    import torch
+
+    gen = torch.Generator().manual_seed(seed)
+    if uniform:
+        lens = torch.full((B,), ctx, dtype=torch.int32)
+    else:
+        lens = torch.randint(ctx // 2, ctx + 1, (B,), generator=gen, dtype=torch.int32)
+    bs = 16
+    nbs = (lens + bs - 1) // bs
+    nbps = int(nbs.max())
+    P = int(nbs.sum())
+    kvdt = torch.bfloat16 if kv_bf16 else torch.float32
+    esz = 2 if kv_bf16 else 4
+    kv_bytes = int(lens.sum()) * H_kv * d * 2 * esz
+    alg = kv_bytes + 2 * B * H_q * d * 4 + 4 * P + 4 * B
+    copies = max(1, -(-(2 * ROTATE_BYTES) // max(kv_bytes, 1))) if kv_bytes < ROTATE_BYTES else 1
+    gcuda = torch.Generator(device="cuda").manual_seed(seed)
+    caches = []
+    for _ in range(copies):
+        kc = torch.randn((P, bs, H_kv, d), device="cuda", generator=gcuda).to(kvdt)
+        vc = torch.randn((P, bs, H_kv, d), device="cuda", generator=gcuda).to(kvdt)
+        perm = torch.randperm(P, generator=gen).to(torch.int32)
+        table = torch.zeros((B, nbps), dtype=torch.int32)
+        off = 0
+        for b in range(B):
+            table[b, : int(nbs[b])] = perm[off: off + int(nbs[b])]
+            off += int(nbs[b])
+        caches.append((kc, vc, table.cuda()))
+    Q = torch.randn((B, H_q, d), device="cuda", generator=gcuda)
+    O = torch.empty_like(Q)
+    lens_d = lens.cuda()
+    max_ctx = int(lens.max())
+    S = ie.num_splits(max_ctx, bs)
+    ws = torch.empty(ie.workspace_bytes(B, H_q, d, S) // 4, dtype=torch.float32, device="cuda")
+    dt = ie.KV_BF16 if kv_bf16 else ie.KV_F32
+
+    def launch(i):
+        kc, vc, table = caches[i % copies]
+        ie.decode_attn(Q, kc, vc, table, lens_d, max_ctx, bs, H_kv, kv_dtype=dt, out=O, workspace=ws)
+
+    n = max(copies, 8)
+    ms = graph_time(launch, n)
+    gbs = alg / (ms * 1e-3) / 1e9
+    res = {"B": B, "H_q": H_q, "H_kv": H_kv, "d": d, "ctx": ctx, "kv": "bf16" if kv_bf16 else "fp32",
+           "lengths": "uniform" if uniform else "U[ctx/2,ctx]", "sum_ctx": int(lens.sum()),
+           "splits": S, "bytes": alg, "us": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+           "frac_hbm": round(gbs / PEAK_HBM_GBS, 3)}
+    log(f"decode_attn {res}")
+    del caches
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_attn(ie):
+    out = [attn_case(ie, 8, 12, 12, 64, 1024, False, True, 3)]
+    for ctx in (4096, 8192, 32768):
+        for bf in (False, True):
+            out.append(attn_case(ie, 32, 32, 8, 128, ctx, bf, False, ctx + bf))
+    return out
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_baseline(inputs, budget_s=12.0):
+    import numpy as np
+    import torch
+
+    from oracle import orc
+
+    Ap, Bp, sA, sB = inputs
+    N, K = Bp.shape[0], Bp.shape[1] * 4
+    B_h = Bp.cpu().numpy()
+    sB_h = sB.cpu().numpy()
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    orc.set_threads(threads)
+    rows = 16
+    A_h = Ap[:rows].cpu().numpy()
+    t0 = time.perf_counter()
+    orc.gemm(A_h, B_h, sA[:rows].cpu().numpy(), sB_h, 0)
+    est = (time.perf_counter() - t0) / rows
+    rows = int(max(16, min(Ap.shape[0], budget_s / max(est, 1e-9))))
+    A_h = Ap[:rows].cpu().numpy()
+    sA_h = sA[:rows].cpu().numpy()
+    t0 = time.perf_counter()
+    C = orc.gemm(A_h, B_h, sA_h, sB_h, 0)
+    dt = time.perf_counter() - t0
+    tops = 2.0 * rows * N * K / dt / 1e12
+    del C
+    return {"value": round(tops, 5), "unit": "TOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of 8192 rows of the 8192^3 INT8 GEMM (Plain), int32 triple loop "
+                      f"+ dequant, OpenMP over rows, {dt:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(this build runs on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    skip = set(s for s in args.skip.split(",") if s)
+    import torch
+
+    import ie_amd as ie
+
+    ie.load()
+    ie.check("ie_init")
+    torch.cuda.synchronize()
+    log("headline: 8192^3 INT8 GEMM")
+    h = bench_headline(ie, args.steps, args.warmup)
+    res = {
+        "metric": METRIC,
+        "value": round(h["value"], 2),
+        "unit": "TOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8 (int32 accumulate, fp32 dequant)",
+        "data": "synthetic: fp32 N(0,1) operands from a seed, quantized per row by the library (untimed)",
+        "config": {"workload": "INT8 GEMM M=N=K=8192, NT layout, Plain epilogue (BASELINE configs[1])",
+                   "M": 8192, "N": 8192, "K": 8192, "parallelism": "none (1 GPU)"},
+        "roofline": roof(h["kernel_tops"], PEAK_I8_TOPS, "TOP/s", "mfma"),
+    }
+    if not args.only_headline:
+        if "gemv" not in skip:
+            res["gemv"] = bench_gemv(ie)
+            big = [r for r in res["gemv"] if r["N"] * r["K"] >= 768 * 50257]
+            best = max(big, key=lambda r: r["GBps"])
+            res["gemv_roofline"] = roof(best["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
+            res["gemv_roofline"]["kernel"] = f"gemv M={best['M']} K={best['K']} N={best['N']}"
+        if "gemm512" not in skip:
+            res["gemm_m512"] = bench_gemm512(ie)
+        if "attn" not in skip:
+            res["decode_attn"] = bench_attn(ie)
+            c8 = [r for r in res["decode_attn"] if r["ctx"] == 8192 and r["kv"] == "fp32"][0]
+            res["decode_attn_roofline"] = roof(c8["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
+            res["decode_attn_roofline"]["kernel"] = "decode_attn cfg4 ctx 8192 fp32"
+    if "cpu" not in skip:
+        log("cpu baseline")
+        res["cpu_baseline"] = cpu_baseline(h["inputs"])
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -21,13 +21,19 @@
 
 namespace ie {
 
-template <int EPI>
+// NT = true writes C with non-temporal stores: used where C is far larger
+// than the caches (it would otherwise evict the operand panels other
+// workgroups are still reading).
+template <int EPI, bool NT = false>
 __device__ __forceinline__ void store_epilogue(void* C, size_t idx, int32_t acc,
                                                float sa, float sb,
                                                const float* bias,
                                                const float* residual, int n) {
     if constexpr (EPI == IE_EPI_I32) {
-        static_cast<int32_t*>(C)[idx] = acc;
+        if constexpr (NT)
+            __builtin_nontemporal_store(acc, static_cast<int32_t*>(C) + idx);
+        else
+            static_cast<int32_t*>(C)[idx] = acc;
     } else {
         const float t = (float)acc * sa;
         float out;
@@ -43,7 +49,10 @@ __device__ __forceinline__ void store_epilogue(void* C, size_t idx, int32_t acc,
         } else {
             out = fmaf(t, sb, bias[n]) + residual[idx];
         }
-        static_cast<float*>(C)[idx] = out;
+        if constexpr (NT)
+            __builtin_nontemporal_store(out, static_cast<float*>(C) + idx);
+        else
+            static_cast<float*>(C)[idx] = out;
     }
 }
 

@@ -1,0 +1,250 @@
+// gemm_i8_mfma256.hip — large-tile INT8 GEMM for gfx950 (M, N >= a few
+// thousand; the 8192^3 configuration).
+//
+// Result identical to the reference's K14 kernel (kernels/quantization/
+// 14_int8_gemm.cu:65-170): exact int32 K-sum, then the dequant epilogue.
+//
+// MI355X mapping:
+//   * 256x256 C tile per 256-thread workgroup; each wave owns 128x128 as
+//     4x4 blocks of v_mfma_i32_32x32x32_i8 (256 int32 accumulators per lane,
+//     held in AGPRs), so every 16-byte A or B fragment read from LDS feeds
+//     four MFMAs;
+//   * K advances 128 bytes per stage; a stage is 2 x 256 rows x 128 B = 64 KiB
+//     and two stages (128 KiB of the 160 KiB LDS) double-buffer the loop;
+//   * global -> LDS copies use global_load_lds_dwordx4 (16 B per lane straight
+//     into LDS, no VGPR round trip); a wave-load fills 1 KiB = 8 rows, the
+//     lane -> global address map applies the LDS swizzle, so the fixed
+//     lane-ordered LDS destination lands each 16-byte chunk at its swizzled
+//     slot;
+//   * LDS rows are 128 B with 16-byte chunk c of row r stored at slot
+//     c ^ ((r >> 1) & 7), which spreads the 32 rows an MFMA operand read
+//     touches over all banks;
+//   * workgroup ids are remapped so each XCD (ids = xcd mod 8) receives a
+//     contiguous run of tiles, walked in groups of GROUP_M tile rows, so the
+//     workgroups resident on one XCD share A and B panels in its L2.
+// Requirements (checked by the launcher): K % 64 == 0, 16-byte aligned A/BT.
+// Rows past M or N read the last valid row (no fault, results discarded).
+#include "device_util.h"
+#include "epilogue.h"
+#include "ie_internal.h"
+
+namespace ie {
+namespace {
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int NSTAGE = 4;              // LDS ring depth
+constexpr int OPER = BM * BK;          // bytes of one operand tile per stage
+constexpr int STAGE = 2 * OPER;        // A + B
+constexpr int GROUP_M = 4;
+constexpr int CHUNKS = BK / 16;        // 16-byte chunks per LDS row
+constexpr int ROWS_PER_LOAD = 64 / CHUNKS;          // rows one wave-load fills
+constexpr int LOADS_PER_WAVE = BM / ROWS_PER_LOAD / 4;  // per operand per stage
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
+
+// 64-byte rows: the 16 rows one quarter-wave of an MFMA operand read touches
+// cover all 64 banks when chunk c of row r sits at slot c ^ ((r >> 2) & 3).
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & (CHUNKS - 1); }
+
+// Copies rows [r0, r0 + ROWS_PER_LOAD) x BK bytes of a K-contiguous operand
+// into LDS with one wave-wide 16-byte-per-lane direct load.
+__device__ __forceinline__ void load_rows(const int8_t* __restrict__ src, int ld, int rows_valid,
+                                          int row0, int k0, int r0, int8_t* lds_oper) {
+    const int lane = threadIdx.x & 63;
+    const int r = r0 + lane / CHUNKS;
+    const int c = (lane % CHUNKS) ^ swz(r);
+    const int gr = min(row0 + r, rows_valid - 1);
+    const int8_t* g = src + (size_t)gr * ld + k0 + c * 16;
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)(lds_oper + r0 * BK), 16, 0, 0);
+}
+
+__device__ __forceinline__ i32x4 read_frag(const int8_t* lds_oper, int row, int chunk) {
+    return *reinterpret_cast<const i32x4*>(lds_oper + row * BK + ((chunk ^ swz(row)) << 4));
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
+    int M, int N, int K, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
+    const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
+    const float* residual, void* C, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) int8_t lds[NSTAGE * STAGE];
+
+    // XCD-aware, grouped tile order.
+    const int nwg = gridDim.x;
+    int id = blockIdx.x;
+    if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
+    const int per_group = GROUP_M * tiles_n;
+    const int group = id / per_group;
+    const int first_m = group * GROUP_M;
+    const int gm = min(tiles_m - first_m, GROUP_M);
+    const int in_group = id - group * per_group;
+    const int tm = first_m + in_group % gm;
+    const int tn = in_group / gm;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    i32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+    const int nk = K / BK;
+    // Copies stage kt_src into LDS slot `slot`.  Every iteration issues one
+    // stage, so the loop body is branch-free: past the last stage the copy
+    // re-reads stage nk-1 into the slot just freed, which is never read again.
+    auto issue = [&](int kt_src, int slot) {
+        int8_t* sa = lds + slot * STAGE;
+        int8_t* sb = sa + OPER;
+        const int k0 = kt_src * BK;
+#pragma unroll
+        for (int j = 0; j < LOADS_PER_WAVE; ++j) {
+            const int r0 = (wave * LOADS_PER_WAVE + j) * ROWS_PER_LOAD;
+            load_rows(A, K, M, m0, k0, r0, sa);
+            load_rows(BT, K, N, n0, k0, r0, sb);
+        }
+    };
+    constexpr int LOADS_PER_STAGE = 2 * LOADS_PER_WAVE;  // per wave
+
+    // Prologue: stages 0 .. NSTAGE-2 in flight, stage 0 landed.
+#pragma unroll
+    for (int p = 0; p < NSTAGE - 1; ++p) issue(min(p, nk - 1), p);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * LOADS_PER_STAGE) : "memory");
+    __builtin_amdgcn_s_barrier();
+
+    const int frow = lane & 31;
+    const int fchunk = lane >> 5;
+    // Operand fragments live in two register slots: slot 0 = k-substep 0 of a
+    // stage, slot 1 = k-substep 1.  An MFMA blocks instruction issue until the
+    // matrix pipe takes it, so LDS reads and global copies are interleaved one
+    // per MFMA (sched_group_barrier) to run in the shadow of the matrix work.
+    i32x4 af[2][4], bf[2][4];
+    auto frags = [&](const int8_t* sa, const int8_t* sb, int ks, int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[slot][i] = read_frag(sa, wm * 128 + i * 32 + frow, ks * 2 + fchunk);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bf[slot][j] = read_frag(sb, wn * 128 + j * 32 + frow, ks * 2 + fchunk);
+    };
+    auto mfma_rows = [&](int slot, int i0, int i1) {
+#pragma unroll
+        for (int i = i0; i < i1; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
+    };
+    frags(lds, lds + OPER, 0, 0);
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int8_t* sa = lds + (kt % NSTAGE) * STAGE;
+        const int8_t* sb = sa + OPER;
+        // -- substep 0: MFMAs on slot 0; in their shadow, the copies for stage
+        //    kt+3 (into the slot freed by iteration kt-1) and the slot-1 reads.
+        __builtin_amdgcn_sched_barrier(0);
+        issue(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
+        frags(sa, sb, 1, 1);
+        mfma_rows(0, 0, 4);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // -- substep 1, first half.
+        mfma_rows(1, 0, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        // Stage kt+1 must have landed (this wave's copies: vmcnt; everyone's:
+        // the barrier); the younger stages stay in flight.  A bare s_barrier,
+        // not __syncthreads(): the latter's workgroup fence drains vmcnt to 0.
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_STAGE) : "memory");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // -- substep 1, second half; in its shadow, slot-0 reads of stage kt+1
+        //    (after the last stage these read a stale slot and go unused).
+        {
+            const int8_t* na = lds + ((kt + 1) % NSTAGE) * STAGE;
+            frags(na, na + OPER, 0, 0);
+        }
+        mfma_rows(1, 2, 4);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+
+    // Epilogue.  All 64 row scales and 4 column scales of this lane are
+    // gathered before the first store, so their latency is paid once, not once
+    // per store.  Lane l of a 32x32 block holds rows 8q + 4(l/32) + r (q, r < 4)
+    // of column l % 32.
+    const int h = lane >> 5;
+    const int rbase = m0 + wm * 128 + 4 * h;
+    const int cbase = n0 + wn * 128 + (lane & 31);
+    float sa[4][16], sb[4];
+    if constexpr (EPI != IE_EPI_I32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                sa[i][v] = sA[min(rbase + i * 32 + 8 * (v >> 2) + (v & 3), M - 1)];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sb[j] = sB[min(cbase + j * 32, N - 1)];
+        // Consume every scale once in straight-line code: the compiler waits
+        // for the loads here, once.  Otherwise the branchy store loop below gets
+        // a conservative vmcnt(0) before each store, and since vmcnt also counts
+        // stores, every store would wait for the previous one to retire.
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) asm volatile("" ::"v"(sa[i][v]));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" ::"v"(sb[j]));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int m = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int n = cbase + j * 32;
+                if (n < N)
+                    store_epilogue<EPI, true>(C, (size_t)m * N + n, acc[i][j][v], sa[i][v], sb[j], bias,
+                                        residual, n);
+            }
+        }
+    }
+}
+
+template <int EPI>
+struct BigLaunch {
+    static void run(const GemmArgs& a, hipStream_t s) {
+        const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
+        gemm_i8_256_kernel<EPI><<<tm * tn, 256, 0, s>>>(
+            a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
+            a.sA, a.sB, a.bias, a.residual, a.C, tm, tn);
+    }
+};
+
+}  // namespace
+
+bool gemm_i8_big_applies(const GemmArgs& a) {
+    if (a.K % BK != 0 || a.K == 0) return false;
+    if (((uintptr_t)a.A % 16) || ((uintptr_t)a.BT % 16)) return false;
+    const long long tiles = (long long)((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    return tiles >= 128 && tiles < (1LL << 31);
+}
+
+void launch_gemm_i8_big(const GemmArgs& a, hipStream_t s) { dispatch_epilogue<BigLaunch>(a.epi, a, s); }
+
+}  // namespace ie

@@ -140,6 +140,7 @@ int orc_int8_gemm_i32(int M, int N, int K, const int32_t* A_packed,
     const int K4 = K / 4;
     int8_t* bt = (int8_t*)malloc((size_t)N * (K ? K : 1));
     if (!bt) return 2;
+#pragma omp parallel for schedule(static)
     for (int j = 0; j < N; ++j) unpack_row(BT_packed + (size_t)j * K4, K, bt + (size_t)j * K);
 #pragma omp parallel
     {
@@ -193,6 +194,7 @@ int orc_int8_gemm(int M, int N, int K, const int32_t* A_packed,
     const int K4 = K / 4;
     int8_t* bt = (int8_t*)malloc((size_t)N * (K ? K : 1));
     if (!bt) return 2;
+#pragma omp parallel for schedule(static)
     for (int j = 0; j < N; ++j) unpack_row(BT_packed + (size_t)j * K4, K, bt + (size_t)j * K);
 #pragma omp parallel
     {

@@ -176,3 +176,45 @@ def test_8192_cube_sampled_rows_and_checksum(ie, orc):
     a_rows = Ap[torch.from_numpy(rows).cuda()].cpu().numpy()
     want = orc.gemm_i32(a_rows, Bp.cpu().numpy())
     assert np.array_equal(C[torch.from_numpy(rows).cuda()].cpu().numpy(), want)
+
+
+# ------------------------------------------------------------------ 256x256 tiles
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (3000, 5000, 512), (2304, 8192, 768),
+                                   (8192, 3000, 256)])
+def test_big_tile_kernel_exact(ie, orc, M, N, K):
+    """Shapes routed to the 256x256-tile kernel (>= 128 tiles, K % 128 == 0),
+    including ragged M and N; int32 exact on sampled rows plus a full column
+    checksum."""
+    import torch
+
+    gen = torch.Generator(device="cuda").manual_seed(M + N + K)
+    A = torch.randint(-128, 128, (M, K), dtype=torch.int8, device="cuda", generator=gen)
+    B = torch.randint(-128, 128, (N, K), dtype=torch.int8, device="cuda", generator=gen)
+    Ap, Bp = A.view(torch.int32), B.view(torch.int32)
+    C = ie.int8_gemm(Ap, Bp, epilogue=ie.EPI_I32, path=ie.PATH_MFMA)
+    torch.cuda.synchronize()
+    colsum = A.to(torch.int64).sum(0).cpu().numpy()
+    assert np.array_equal(C.to(torch.int64).sum(0).cpu().numpy(), B.cpu().numpy().astype(np.int64) @ colsum)
+    rows = np.unique(np.clip(np.array([0, 1, 255, 256, M // 2, M - 257, M - 2, M - 1]), 0, M - 1))
+    idx = torch.from_numpy(rows).cuda()
+    want = orc.gemm_i32(Ap[idx].cpu().numpy(), Bp.cpu().numpy())
+    assert np.array_equal(C[idx].cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_big_tile_epilogues(ie, orc, epi):
+    M, N, K = 2304, 4100, 768
+    A, W = problem(M, N, K, 40 + epi)
+    r = rng(41)
+    bias = r.standard_normal(N).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi, dev(bias) if epi else None,
+                            dev(res) if epi == 3 else None, path=ie.PATH_MFMA))
+    rows = [0, 1, 1000, 2303]
+    want = orc.gemm(Ap[rows], Wp, sA[rows], sW, epi, bias if epi else None, res[rows] if epi == 3 else None)
+    if epi == 2:
+        assert np.allclose(got[rows], want, rtol=2e-6, atol=1e-7)
+    else:
+        assert np.array_equal(got[rows], want)
