@@ -149,7 +149,8 @@ def bench_headline(ie, steps, warmup):
 def bench_gemv(ie):
     import torch
 
-    shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 50257), (8192, 8192)]
+    shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 50257), (8192, 8192),
+              (8192, 28672)]
     out = []
     g = torch.Generator(device="cuda").manual_seed(7)
     for K, N in shapes:

@@ -28,6 +28,112 @@ namespace {
 constexpr int kRowsPerWG = 16;
 constexpr int kChunk = 128;  // 16-byte columns of A per LDS chunk (2 KiB of K)
 
+// Shared tail: reduce each row's 16 lane partials with DPP and store.
+template <int MT, int EPI>
+__device__ __forceinline__ void gemv_finish(const int32_t (&acc)[MT], int li, int n, bool row_ok,
+                                            int M, int N, const float* __restrict__ sA,
+                                            const float* __restrict__ sB, const float* bias,
+                                            const float* residual, void* C) {
+    int32_t mine = 0;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int32_t t = row16_sum(acc[m]);
+        if (li == m) mine = t;
+    }
+    if (row_ok && li < M) {
+        const size_t idx = (size_t)li * N + n;
+        float sa = 0.0f, sb = 0.0f;
+        if constexpr (EPI != IE_EPI_I32) {
+            sa = sA[li];
+            sb = sB[n];
+        }
+        store_epilogue<EPI>(C, idx, mine, sa, sb, bias, residual, n);
+    }
+}
+
+template <int MT>
+__device__ __forceinline__ void dot_chunk(int32_t (&acc)[MT], const i32x4 wv, const i32x4* a_lds,
+                                          int stride, int c) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const i32x4 av = a_lds[m * stride + c];
+        int32_t s = acc[m];
+        s = dot4_i8(wv.x, av.x, s);
+        s = dot4_i8(wv.y, av.y, s);
+        s = dot4_i8(wv.z, av.z, s);
+        s = dot4_i8(wv.w, av.w, s);
+        acc[m] = s;
+    }
+}
+
+// K known at compile time (K16 = K / 16 sixteen-byte chunks per row).  Each
+// wave walks groups of G x 4 rows; all weight loads of a group (G * K16 / 16
+// per lane, 12 for the GPT-2 shapes) are issued together, and the next
+// group's loads are issued before the current group is reduced, so every lane
+// keeps 12-24 16-byte HBM reads in flight.  The first group's loads are issued
+// before the activation block A[M, K] is staged in LDS, so the staging
+// latency hides behind them.
+template <int MT, int EPI, int K16>
+__global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
+    int M, int N, const int32_t* __restrict__ A, const int32_t* __restrict__ BT,
+    const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
+    const float* residual, void* C) {
+    constexpr int CPL = K16 / 16;                             // chunks per lane per row
+    constexpr int G = CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;   // row groups per pass
+    static_assert(CPL <= 32, "fixed-K GEMV covers K <= 8192");
+    __shared__ i32x4 a_lds[MT * K16];
+    const int lane = threadIdx.x & 63;
+    const int li = lane & 15;
+    const int wave_global = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int step = gridDim.x * 4 * (4 * G);
+    const i32x4* w4 = reinterpret_cast<const i32x4*>(BT);
+
+    i32x4 wv[G][CPL];
+    auto load_group = [&](int r0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int n = r0 + g * 4 + (lane >> 4);
+            const i32x4* w = w4 + (size_t)min(n, N - 1) * K16 + li;
+#pragma unroll
+            for (int t = 0; t < CPL; ++t) wv[g][t] = w[16 * t];
+        }
+    };
+    int r0 = wave_global * (4 * G);
+    if (r0 < N) load_group(r0);
+
+    const i32x4* a4 = reinterpret_cast<const i32x4*>(A);
+    for (int i = threadIdx.x; i < MT * K16; i += 256) {
+        const int m = i / K16;
+        const int mm = m < M ? m : M - 1;
+        a_lds[i] = a4[(size_t)mm * K16 + (i - m * K16)];
+    }
+    __syncthreads();
+
+    for (; r0 < N; r0 += step) {
+        if constexpr (CPL > 16)
+            if (r0 != wave_global * (4 * G)) load_group(r0);
+        int32_t acc[G][MT];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[g][m] = 0;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int t = 0; t < CPL; ++t) dot_chunk<MT>(acc[g], wv[g][t], a_lds, K16, li + 16 * t);
+        // Next pass in flight during the reduce (K <= 4096: 12-16 loads per
+        // lane; at K = 8192 one pass already keeps 32 loads per lane in flight).
+        if constexpr (CPL <= 16)
+            if (r0 + step < N) load_group(r0 + step);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int n = r0 + g * 4 + (lane >> 4);
+            gemv_finish<MT, EPI>(acc[g], li, n, n < N, M, N, sA, sB, bias, residual, C);
+        }
+    }
+}
+
+// Any K % 16 == 0: activations staged in LDS in 2 KiB-of-K chunks.
 template <int MT, int EPI>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(
     int M, int N, int K, const int32_t* __restrict__ A,
@@ -58,37 +164,71 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
         }
         __syncthreads();
         if (row_ok) {
-#pragma unroll 4
-            for (int c = li; c < cw; c += 16) {
-                const i32x4 wv = w[c0 + c];
+#pragma unroll 8
+            for (int c = li; c < cw; c += 16) dot_chunk<MT>(acc, w[c0 + c], a_lds, kChunk, c);
+        }
+    }
+    gemv_finish<MT, EPI>(acc, li, n, row_ok, M, N, sA, sB, bias, residual, C);
+}
+
+// 5 <= M <= 16: v_mfma_i32_16x16x64_i8 with the activations (M padded to 16
+// rows, staged in LDS once per workgroup) as the A operand and 16 weight rows
+// per wave as the B operand.  Lane l feeds weight row n0 + l % 16, K-bytes
+// 16 * (l / 16) .. +16 of each 64-byte K step, so one 16-byte load per lane per
+// MFMA streams 1 KiB of weights; dot4 would need 4 instructions per weight
+// byte at M = 16, which caps it below HBM speed.  Accumulator v of lane l is
+// C[4 * (l / 16) + v][n0 + l % 16].
+template <int EPI, int K64>
+__global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
+    int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
+    const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
+    const float* residual, void* C) {
+    constexpr int K = K64 * 64;
+    constexpr int U = K64 % 8 == 0 ? 8 : (K64 % 4 == 0 ? 4 : 2);  // loads in flight per lane
+    __shared__ i32x4 a_lds[16 * K / 16];
+    for (int i = threadIdx.x; i < 16 * (K / 16); i += 256) {
+        const int m = i / (K / 16);
+        const int mm = m < M ? m : M - 1;
+        a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)mm * K)[i - m * (K / 16)];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15, kq = lane >> 4;
+    const int wave_global = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int waves = gridDim.x * 4;
+    for (int n0 = wave_global * 16; n0 < N; n0 += waves * 16) {
+        const int8_t* w = BT + (size_t)min(n0 + col, N - 1) * K + kq * 16;
+        const i32x4* a = a_lds + col * (K / 16) + kq;
+        // Two accumulators alternate so consecutive MFMAs do not wait on each
+        // other; their integer sum is exact.
+        i32x4 acc = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+#pragma unroll 1
+        for (int k0 = 0; k0 < K64; k0 += U) {
+            i32x4 wv[U];
 #pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const i32x4 av = a_lds[m * kChunk + c];
-                    int32_t s = acc[m];
-                    s = dot4_i8(wv.x, av.x, s);
-                    s = dot4_i8(wv.y, av.y, s);
-                    s = dot4_i8(wv.z, av.z, s);
-                    s = dot4_i8(wv.w, av.w, s);
-                    acc[m] = s;
+            for (int u = 0; u < U; ++u) wv[u] = *reinterpret_cast<const i32x4*>(w + (k0 + u) * 64);
+#pragma unroll
+            for (int u = 0; u < U; u += 2) {
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[(k0 + u) * 4], wv[u], acc, 0, 0, 0);
+                if (u + 1 < U)
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[(k0 + u + 1) * 4], wv[u + 1], acc1, 0, 0, 0);
+            }
+        }
+        acc += acc1;
+        const int n = n0 + col;
+        if (n < N) {
+            float sb = 0.0f;
+            if constexpr (EPI != IE_EPI_I32) sb = sB[n];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = 4 * kq + v;
+                if (m < M) {
+                    float sa = 0.0f;
+                    if constexpr (EPI != IE_EPI_I32) sa = sA[m];
+                    store_epilogue<EPI>(C, (size_t)m * N + n, acc[v], sa, sb, bias, residual, n);
                 }
             }
         }
-    }
-
-    int32_t mine = 0;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        const int32_t t = row16_sum(acc[m]);
-        if (li == m) mine = t;
-    }
-    if (row_ok && li < M) {
-        const size_t idx = (size_t)li * N + n;
-        float sa = 0.0f, sb = 0.0f;
-        if constexpr (EPI != IE_EPI_I32) {
-            sa = sA[li];
-            sb = sB[n];
-        }
-        store_epilogue<EPI>(C, idx, mine, sa, sb, bias, residual, n);
     }
 }
 
@@ -116,19 +256,50 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
     store_epilogue<EPI>(C, idx, s, sa, sb, bias, residual, n);
 }
 
+template <int MT, int EPI, int K16>
+void launch_fixed(const GemmArgs& a, hipStream_t s) {
+    constexpr int CPL = K16 / 16;
+    constexpr int G = CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;
+    const int rows_per_wg = 4 * 4 * G;
+    const unsigned blocks = (unsigned)min((a.N + rows_per_wg - 1) / rows_per_wg, 2048);
+    gemv_i8_fixed_kernel<MT, EPI, K16><<<blocks, 256, 0, s>>>(a.M, a.N, a.A, a.BT, a.sA, a.sB,
+                                                              a.bias, a.residual, a.C);
+}
+
+template <int EPI, int K64>
+void launch_mfma16(const GemmArgs& a, hipStream_t s) {
+    const unsigned blocks = (unsigned)min((a.N + 63) / 64, 2048);
+    gemv_i8_mfma16_kernel<EPI, K64><<<blocks, 256, 0, s>>>(
+        a.M, a.N, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
+        a.sA, a.sB, a.bias, a.residual, a.C);
+}
+
+template <int MT, int EPI>
+void launch_mt(const GemmArgs& a, hipStream_t s) {
+    if constexpr (MT > 4) {
+        if (a.K == 768) return launch_mfma16<EPI, 12>(a, s);
+        if (a.K == 3072) return launch_mfma16<EPI, 48>(a, s);
+    }
+    // Specialised K: the GPT-2 widths and the square 8192 shape, while the
+    // activation block fits the 48 KiB LDS budget.
+    if constexpr (MT <= 4) {
+        if (a.K == 768) return launch_fixed<MT, EPI, 48>(a, s);
+        if (a.K == 3072) return launch_fixed<MT, EPI, 192>(a, s);
+        if (a.K == 8192 && MT == 1) return launch_fixed<MT, EPI, 512>(a, s);
+    }
+    const dim3 grid((a.N + kRowsPerWG - 1) / kRowsPerWG);
+    gemv_i8_kernel<MT, EPI><<<grid, 256, 0, s>>>(a.M, a.N, a.K, a.A, a.BT, a.sA, a.sB, a.bias,
+                                                  a.residual, a.C);
+}
+
 template <int EPI>
 struct GemvLaunch {
     static void run(const GemmArgs& a, hipStream_t s) {
-        const dim3 grid((a.N + kRowsPerWG - 1) / kRowsPerWG);
-#define IE_GEMV(MT)                                                                 \
-    gemv_i8_kernel<MT, EPI><<<grid, 256, 0, s>>>(a.M, a.N, a.K, a.A, a.BT, a.sA, a.sB, \
-                                                 a.bias, a.residual, a.C)
-        if (a.M <= 1) IE_GEMV(1);
-        else if (a.M <= 2) IE_GEMV(2);
-        else if (a.M <= 4) IE_GEMV(4);
-        else if (a.M <= 8) IE_GEMV(8);
-        else IE_GEMV(16);
-#undef IE_GEMV
+        if (a.M <= 1) launch_mt<1, EPI>(a, s);
+        else if (a.M <= 2) launch_mt<2, EPI>(a, s);
+        else if (a.M <= 4) launch_mt<4, EPI>(a, s);
+        else if (a.M <= 8) launch_mt<8, EPI>(a, s);
+        else launch_mt<16, EPI>(a, s);
     }
 };
 
