@@ -31,8 +31,46 @@
 namespace ie {
 namespace {
 
+// Raw K/V words of one lane's d/16-element slice of one token; bf16 stays
+// packed until use so a prefetched chunk costs half the registers.
+template <int EPL, typename KV>
+struct Slice {
+    static constexpr int WORDS = EPL * (int)sizeof(KV) / 4;
+    uint32_t w[WORDS];
+};
+
+template <int EPL, typename KV>
+__device__ __forceinline__ void load_raw(const KV* __restrict__ p, Slice<EPL, KV>& s) {
+    constexpr int W = Slice<EPL, KV>::WORDS;
+    if constexpr (W % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < W / 4; ++i) {
+            const uint4 v = reinterpret_cast<const uint4*>(p)[i];
+            s.w[4 * i + 0] = v.x;
+            s.w[4 * i + 1] = v.y;
+            s.w[4 * i + 2] = v.z;
+            s.w[4 * i + 3] = v.w;
+        }
+    } else {
+        static_assert(W == 2, "slice width");
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        s.w[0] = v.x;
+        s.w[1] = v.y;
+    }
+}
+
+template <int EPL, typename KV>
+__device__ __forceinline__ float elem(const Slice<EPL, KV>& s, int e) {
+    if constexpr (sizeof(KV) == 4) {
+        return __builtin_bit_cast(float, s.w[e]);
+    } else {
+        const uint32_t w = s.w[e >> 1];
+        return __builtin_bit_cast(float, (e & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+}
+
 template <int EPL>
-__device__ __forceinline__ void load_slice(const float* __restrict__ p, float (&out)[EPL]) {
+__device__ __forceinline__ void load_q(const float* __restrict__ p, float (&out)[EPL]) {
 #pragma unroll
     for (int i = 0; i < EPL / 4; ++i) {
         const float4 v = reinterpret_cast<const float4*>(p)[i];
@@ -43,25 +81,68 @@ __device__ __forceinline__ void load_slice(const float* __restrict__ p, float (&
     }
 }
 
-template <int EPL>
-__device__ __forceinline__ void load_slice(const uint16_t* __restrict__ p, float (&out)[EPL]) {
-    if constexpr (EPL == 8) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+template <int D, typename KV>
+struct Chunk {
+    static constexpr int EPL = D / 16;
+    Slice<EPL, KV> k[4], v[4];
+    bool valid[4];
+};
+
+// Loads this lane's slices of tokens c0 + 4j + grp (j < 4) of a 16-token chunk.
+template <int D, typename KV>
+__device__ __forceinline__ void load_chunk(Chunk<D, KV>& c, int c0, int grp, int tok1,
+                                           const int* __restrict__ bt, int block_size,
+                                           size_t tok_stride, const KV* kbase, const KV* vbase) {
+// Branch-free: positions past tok1 re-read token tok1-1 (a cache hit) and are
+// masked by `valid`, so the loads never sit in divergent control flow and the
+// compiler can keep the next chunk in flight across the current one.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            out[2 * i + 0] = __builtin_bit_cast(float, w[i] << 16);
-            out[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
-        }
-    } else {
-        static_assert(EPL == 4, "slice width");
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        const uint32_t w[2] = {v.x, v.y};
+    for (int j = 0; j < 4; ++j) {
+        const int pos = c0 + 4 * j + grp;
+        c.valid[j] = pos < tok1;
+        const int pc = min(pos, tok1 - 1);
+        const int blk = pc / block_size;
+        const size_t row = (size_t)bt[blk] * block_size + (pc - blk * block_size);
+        load_raw(kbase + row * tok_stride, c.k[j]);
+        load_raw(vbase + row * tok_stride, c.v[j]);
+    }
+}
+
+template <int D, int G, typename KV>
+__device__ __forceinline__ void consume_chunk(const Chunk<D, KV>& c, const float (&q)[G][D / 16],
+                                              float (&m)[G], float (&l)[G], float (&o)[G][D / 16]) {
+    constexpr int EPL = D / 16;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            out[2 * i + 0] = __builtin_bit_cast(float, w[i] << 16);
-            out[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+    for (int g = 0; g < G; ++g) {
+        float s[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) dot = fmaf(q[g][e], elem(c.k[j], e), dot);
+            dot = row16_sum(dot);
+            s[j] = c.valid[j] ? dot : -INFINITY;
         }
+        float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        cm = fmaxf(cm, xor16(cm));
+        cm = fmaxf(cm, xor32(cm));
+        const float mn = fmaxf(m[g], cm);
+        const float alpha = exp2f(m[g] - mn);
+        float p[4], psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            p[j] = exp2f(s[j] - mn);
+            psum += p[j];
+        }
+        l[g] = fmaf(l[g], alpha, psum);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            float acc = o[g][e] * alpha;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = fmaf(p[j], elem(c.v[j], e), acc);
+            o[g][e] = acc;
+        }
+        m[g] = mn;
     }
 }
 
@@ -72,7 +153,6 @@ __global__ __launch_bounds__(256) void decode_attn_split_kernel(
     int H_kv, int block_size, int nbps, int num_splits, int blocks_per_split, float qscale,
     float* __restrict__ ws) {
     constexpr int EPL = D / 16;
-    constexpr int TPS = 4;  // tokens per lane row per chunk (4 rows x 4 = 16)
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane >> 4, li = lane & 15;
@@ -86,10 +166,21 @@ __global__ __launch_bounds__(256) void decode_attn_split_kernel(
     const int tok0 = (int)min(t0l, lim);
     const int tok1 = (int)min(t0l + span, lim);
 
+    const int* bt = block_table + (size_t)b * nbps;
+    const size_t tok_stride = (size_t)H_kv * D;
+    const KV* kbase = kcache + (size_t)kvh * D + li * EPL;
+    const KV* vbase = vcache + (size_t)kvh * D + li * EPL;
+
+    // Chunks of 16 tokens go to the four waves round-robin; each wave keeps
+    // the next chunk's loads in flight while it computes the current one.
+    Chunk<D, KV> ca, cb;
+    int c0 = tok0 + wave * 16;
+    if (c0 < tok1) load_chunk(ca, c0, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+
     float q[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        load_slice<EPL>(Q + ((size_t)b * H_q + (size_t)kvh * G + g) * D + li * EPL, q[g]);
+        load_q<EPL>(Q + ((size_t)b * H_q + (size_t)kvh * G + g) * D + li * EPL, q[g]);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) q[g][e] *= qscale;
     }
@@ -103,61 +194,16 @@ __global__ __launch_bounds__(256) void decode_attn_split_kernel(
         for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
     }
 
-    const int* bt = block_table + (size_t)b * nbps;
-    const size_t tok_stride = (size_t)H_kv * D;
-    const KV* kbase = kcache + (size_t)kvh * D + li * EPL;
-    const KV* vbase = vcache + (size_t)kvh * D + li * EPL;
-
-    for (int c0 = tok0 + wave * 16; c0 < tok1; c0 += 64) {
-        float kk[TPS][EPL], vv[TPS][EPL];
-        bool valid[TPS];
-#pragma unroll
-        for (int j = 0; j < TPS; ++j) {
-            const int pos = c0 + TPS * j + grp;
-            valid[j] = pos < tok1;
-            if (valid[j]) {
-                const int blk = pos / block_size;
-                const int off = pos - blk * block_size;
-                const size_t row = (size_t)bt[blk] * block_size + off;
-                load_slice<EPL>(kbase + row * tok_stride, kk[j]);
-                load_slice<EPL>(vbase + row * tok_stride, vv[j]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) kk[j][e] = vv[j][e] = 0.0f;
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float s[TPS];
-#pragma unroll
-            for (int j = 0; j < TPS; ++j) {
-                float dot = 0.0f;
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) dot = fmaf(q[g][e], kk[j][e], dot);
-                dot = row16_sum(dot);
-                s[j] = valid[j] ? dot : -INFINITY;
-            }
-            float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-            cm = fmaxf(cm, xor16(cm));
-            cm = fmaxf(cm, xor32(cm));
-            const float mn = fmaxf(m[g], cm);
-            const float alpha = exp2f(m[g] - mn);
-            float p[TPS], psum = 0.0f;
-#pragma unroll
-            for (int j = 0; j < TPS; ++j) {
-                p[j] = exp2f(s[j] - mn);
-                psum += p[j];
-            }
-            l[g] = fmaf(l[g], alpha, psum);
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                float acc = o[g][e] * alpha;
-#pragma unroll
-                for (int j = 0; j < TPS; ++j) acc = fmaf(p[j], vv[j][e], acc);
-                o[g][e] = acc;
-            }
-            m[g] = mn;
-        }
+    // Ping-pong: the loads for chunk c0+64 are always issued (clamped past the
+    // end) before chunk c0 is consumed.
+    while (c0 < tok1) {
+        load_chunk(cb, c0 + 64, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+        consume_chunk<D, G, KV>(ca, q, m, l, o);
+        c0 += 64;
+        if (c0 >= tok1) break;
+        load_chunk(ca, c0 + 64, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+        consume_chunk<D, G, KV>(cb, q, m, l, o);
+        c0 += 64;
     }
 
     // The four lane rows share the wave's running max: plain sums merge them.
