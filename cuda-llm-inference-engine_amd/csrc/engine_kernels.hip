@@ -1,0 +1,67 @@
+// engine_kernels.hip — small kernels private to the decode-step engine.
+//
+// qkv_split_append fuses the reference's qkv_split_kernel and
+// kv_cache_write_kernel (src/gpt2_engine.cu:292-315, 321-346): from the QKV
+// projection [B, 3d] (per token Q || K || V, HF c_attn order) it writes Q
+// [B, d] contiguously for attention, appends K and V at each sequence's
+// current position through its block-table row, and sets the attention
+// context length pos + 1.  advance moves every sequence one position on.
+// Positions and token ids live in device memory, so a captured decode step
+// replays without host involvement.
+#include "device_util.h"
+#include "ie_internal.h"
+
+namespace ie {
+namespace {
+
+template <typename KV>
+__device__ __forceinline__ KV to_kv(float x);
+template <>
+__device__ __forceinline__ float to_kv<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ uint16_t to_kv<uint16_t>(float x) { return f32_to_bf16_rne(x); }
+
+template <typename KV>
+__global__ __launch_bounds__(256) void qkv_split_append_kernel(
+    int B, int d, const float* __restrict__ qkv, const int* __restrict__ positions,
+    const int* __restrict__ block_table, int nbps, int block_size, float* __restrict__ Q,
+    KV* __restrict__ kc, KV* __restrict__ vc, int* __restrict__ ctx_lens) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= B * d) return;
+    const int b = idx / d, i = idx - (idx / d) * d;
+    const float* row = qkv + (size_t)b * 3 * d;
+    const int pos = positions[b];
+    const int blk = pos / block_size;
+    const size_t slot = (size_t)block_table[(size_t)b * nbps + blk] * block_size + (pos - blk * block_size);
+    Q[idx] = row[i];
+    kc[slot * d + i] = to_kv<KV>(row[d + i]);
+    vc[slot * d + i] = to_kv<KV>(row[2 * d + i]);
+    if (i == 0) ctx_lens[b] = pos + 1;
+}
+
+__global__ void advance_kernel(int B, int* __restrict__ positions) {
+    const int b = blockIdx.x * 64 + threadIdx.x;
+    if (b < B) positions[b] += 1;
+}
+
+}  // namespace
+
+void launch_qkv_split_append(int B, int d, const float* qkv, const int* positions,
+                             const int* block_table, int nbps, int block_size, float* Q,
+                             void* kc, void* vc, int kv_dtype, int* ctx_lens, hipStream_t s) {
+    const unsigned blocks = (unsigned)((B * d + 255) / 256);
+    if (kv_dtype == IE_KV_BF16)
+        qkv_split_append_kernel<uint16_t><<<blocks, 256, 0, s>>>(
+            B, d, qkv, positions, block_table, nbps, block_size, Q, static_cast<uint16_t*>(kc),
+            static_cast<uint16_t*>(vc), ctx_lens);
+    else
+        qkv_split_append_kernel<float><<<blocks, 256, 0, s>>>(
+            B, d, qkv, positions, block_table, nbps, block_size, Q, static_cast<float*>(kc),
+            static_cast<float*>(vc), ctx_lens);
+}
+
+void launch_advance(int B, int* positions, hipStream_t s) {
+    advance_kernel<<<(B + 63) / 64, 64, 0, s>>>(B, positions);
+}
+
+}  // namespace ie

@@ -70,6 +70,12 @@ void launch_kv_append_batch(int B, const float* K, const float* V, void* kc,
                             const int* positions, int H, int dh, int bs,
                             hipStream_t s);
 
+// ---- decode-step engine kernels (engine_kernels.hip) ----
+void launch_qkv_split_append(int B, int d, const float* qkv, const int* positions,
+                             const int* block_table, int nbps, int block_size, float* Q,
+                             void* kc, void* vc, int kv_dtype, int* ctx_lens, hipStream_t s);
+void launch_advance(int B, int* positions, hipStream_t s);
+
 // ---- support ops (support.hip) ----
 void launch_layernorm(int rows, int cols, const float* x, const float* g,
                       const float* b, float* out, float eps, hipStream_t s);

@@ -1,0 +1,657 @@
+// gpt2_engine.cpp — GPT-2 decode engine over the INT8 decode hot path.
+//
+// The decode step follows the reference's GPT2Engine::forward_layer decode
+// branch (src/gpt2_engine.cu:447-528) and generate loop (:629-783):
+//   embed -> 12 x [LN1 -> quantize -> QKV GEMM+bias -> split/KV append ->
+//   split-K paged decode attention -> quantize -> out GEMM+bias+residual ->
+//   LN2 -> quantize -> up GEMM+bias+GELU -> quantize -> down GEMM+bias+
+//   residual] -> final LN -> LM head -> argmax.
+// Differences in mechanism, not in arithmetic: no device-to-device residual
+// copies (the residual stream x is read by LayerNorm and updated in place by
+// the residual epilogues); the QKV split and KV write are one kernel; block
+// tables, positions and token ids live on the device and a captured HIP graph
+// replays a whole step; argmax runs on the device and only B token ids come
+// back per step (the reference copies all 50257 logits to the host).
+#include "ie_gpt2_engine.h"
+
+#include <hip/hip_runtime.h>
+#include <sys/stat.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <numeric>
+#include <random>
+#include <sstream>
+#include <stdexcept>
+
+#include "../csrc/ie_internal.h"
+
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPC(x) hip_check((x), #x)
+
+void ie_check(int st, const char* what) {
+    if (st != IE_OK) throw std::runtime_error(std::string(what) + ": " + ie_last_error());
+}
+#define IEC(x) ie_check((x), #x)
+
+// ---------------------------------------------------------------- host RNG
+// SplitMix64 (Steele, Lea, Flood 2014) feeding Box-Muller normals; one stream
+// per tensor so every tensor is reproducible on its own.
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed) {}
+    uint64_t next() {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    double uniform() { return ((next() >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+};
+
+std::vector<float> normal(size_t n, float stddev, uint64_t seed) {
+    std::vector<float> v(n);
+    Rng r(seed);
+    for (size_t i = 0; i < n; i += 2) {
+        const double u1 = r.uniform(), u2 = r.uniform();
+        const double rad = std::sqrt(-2.0 * std::log(u1));
+        v[i] = (float)(rad * std::cos(6.283185307179586 * u2)) * stddev;
+        if (i + 1 < n) v[i + 1] = (float)(rad * std::sin(6.283185307179586 * u2)) * stddev;
+    }
+    return v;
+}
+
+// python/export_gpt2.py:10-40 (quantize_per_row): per-row symmetric int8 in
+// float32 arithmetic, round half to even, little-endian packing.
+void quantize_rows_host(const std::vector<float>& w, int rows, int cols, std::vector<int32_t>& packed,
+                        std::vector<float>& scales) {
+    packed.assign((size_t)rows * cols / 4, 0);
+    scales.assign(rows, 1.0f);
+    for (int r = 0; r < rows; ++r) {
+        const float* x = w.data() + (size_t)r * cols;
+        float m = 0.0f;
+        for (int c = 0; c < cols; ++c) m = std::max(m, std::fabs(x[c]));
+        const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+        scales[r] = scale;
+        for (int i = 0; i < cols / 4; ++i) {
+            uint32_t word = 0;
+            for (int j = 0; j < 4; ++j) {
+                float q = std::nearbyint(x[4 * i + j] * inv);
+                q = std::min(std::max(q, -128.0f), 127.0f);
+                word |= (uint32_t)(uint8_t)(int8_t)q << (8 * j);
+            }
+            packed[(size_t)r * (cols / 4) + i] = (int32_t)word;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- model I/O
+template <typename T>
+std::vector<T> read_bin(const std::string& path, size_t count) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot open " + path);
+    std::vector<T> v(count);
+    f.read(reinterpret_cast<char*>(v.data()), (std::streamsize)(count * sizeof(T)));
+    if ((size_t)f.gcount() != count * sizeof(T)) throw std::runtime_error("short file " + path);
+    return v;
+}
+
+template <typename T>
+void write_bin(const std::string& path, const std::vector<T>& v) {
+    std::ofstream f(path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot write " + path);
+    f.write(reinterpret_cast<const char*>(v.data()), (std::streamsize)(v.size() * sizeof(T)));
+}
+
+// src/gpt2_engine.cu:41-60: the config keys, read by name.
+GPT2Config read_config(const std::string& path) {
+    std::ifstream f(path);
+    if (!f) throw std::runtime_error("cannot open " + path);
+    std::stringstream ss;
+    ss << f.rdbuf();
+    const std::string s = ss.str();
+    auto get = [&](const char* key) {
+        const auto k = s.find(std::string("\"") + key + "\"");
+        if (k == std::string::npos) throw std::runtime_error(std::string("config.json lacks ") + key);
+        const auto c = s.find(':', k);
+        return std::atoi(s.c_str() + c + 1);
+    };
+    GPT2Config c;
+    c.n_layers = get("n_layers");
+    c.n_heads = get("n_heads");
+    c.d_model = get("d_model");
+    c.d_ff = get("d_ff");
+    c.vocab_size = get("vocab_size");
+    c.max_seq_len = get("max_seq_len");
+    c.d_head = get("d_head");
+    return c;
+}
+
+void validate(const GPT2Config& c) {
+    if (c.n_layers <= 0 || c.n_heads <= 0 || c.d_model <= 0 || c.d_ff <= 0 || c.vocab_size <= 0 ||
+        c.max_seq_len <= 0 || c.d_head * c.n_heads != c.d_model)
+        throw std::runtime_error("invalid GPT2Config");
+    if (c.d_model % 16 || c.d_ff % 16) throw std::runtime_error("d_model and d_ff must be multiples of 16");
+    if (c.d_head != 64 && c.d_head != 128) throw std::runtime_error("d_head must be 64 or 128");
+}
+
+// Host copy of every tensor, in the on-disk layout.
+struct HostModel {
+    GPT2Config cfg;
+    std::vector<float> wte, wpe, lnf_g, lnf_b;
+    struct Layer {
+        std::vector<float> ln1_g, ln1_b, ln2_g, ln2_b, qkv_b, out_b, up_b, down_b;
+        std::vector<float> qkv_s, out_s, up_s, down_s;
+        std::vector<int32_t> qkv_w, out_w, up_w, down_w;
+    };
+    std::vector<Layer> layers;
+};
+
+HostModel random_model(const GPT2Config& c, uint64_t seed) {
+    validate(c);
+    HostModel m;
+    m.cfg = c;
+    const int d = c.d_model, ff = c.d_ff;
+    uint64_t tid = 0;
+    auto nxt = [&](size_t n) { return normal(n, 0.02f, seed * 0x100000001B3ull + (++tid)); };
+    m.wte = nxt((size_t)c.vocab_size * d);
+    m.wpe = nxt((size_t)c.max_seq_len * d);
+    m.lnf_g.assign(d, 1.0f);
+    m.lnf_b.assign(d, 0.0f);
+    m.layers.resize(c.n_layers);
+    for (auto& L : m.layers) {
+        L.ln1_g.assign(d, 1.0f);
+        L.ln1_b.assign(d, 0.0f);
+        L.ln2_g.assign(d, 1.0f);
+        L.ln2_b.assign(d, 0.0f);
+        // weights drawn directly in the exporter's transposed [N=out, K=in] layout
+        quantize_rows_host(nxt((size_t)3 * d * d), 3 * d, d, L.qkv_w, L.qkv_s);
+        L.qkv_b = nxt(3 * d);
+        quantize_rows_host(nxt((size_t)d * d), d, d, L.out_w, L.out_s);
+        L.out_b = nxt(d);
+        quantize_rows_host(nxt((size_t)ff * d), ff, d, L.up_w, L.up_s);
+        L.up_b = nxt(ff);
+        quantize_rows_host(nxt((size_t)d * ff), d, ff, L.down_w, L.down_s);
+        L.down_b = nxt(d);
+    }
+    return m;
+}
+
+HostModel load_model(const std::string& dir) {
+    HostModel m;
+    m.cfg = read_config(dir + "/config.json");
+    const GPT2Config& c = m.cfg;
+    validate(c);
+    const int d = c.d_model, ff = c.d_ff;
+    m.wte = read_bin<float>(dir + "/wte.bin", (size_t)c.vocab_size * d);
+    m.wpe = read_bin<float>(dir + "/wpe.bin", (size_t)c.max_seq_len * d);
+    m.lnf_g = read_bin<float>(dir + "/ln_f_gamma.bin", d);
+    m.lnf_b = read_bin<float>(dir + "/ln_f_beta.bin", d);
+    m.layers.resize(c.n_layers);
+    for (int i = 0; i < c.n_layers; ++i) {
+        char ld[64];
+        std::snprintf(ld, sizeof(ld), "/layer_%02d/", i);
+        const std::string p = dir + ld;
+        auto& L = m.layers[i];
+        L.ln1_g = read_bin<float>(p + "ln1_gamma.bin", d);
+        L.ln1_b = read_bin<float>(p + "ln1_beta.bin", d);
+        L.ln2_g = read_bin<float>(p + "ln2_gamma.bin", d);
+        L.ln2_b = read_bin<float>(p + "ln2_beta.bin", d);
+        L.qkv_w = read_bin<int32_t>(p + "qkv_weight.bin", (size_t)3 * d * d / 4);
+        L.qkv_s = read_bin<float>(p + "qkv_scale.bin", 3 * d);
+        L.qkv_b = read_bin<float>(p + "qkv_bias.bin", 3 * d);
+        L.out_w = read_bin<int32_t>(p + "out_weight.bin", (size_t)d * d / 4);
+        L.out_s = read_bin<float>(p + "out_scale.bin", d);
+        L.out_b = read_bin<float>(p + "out_bias.bin", d);
+        L.up_w = read_bin<int32_t>(p + "ffn_up_weight.bin", (size_t)ff * d / 4);
+        L.up_s = read_bin<float>(p + "ffn_up_scale.bin", ff);
+        L.up_b = read_bin<float>(p + "ffn_up_bias.bin", ff);
+        L.down_w = read_bin<int32_t>(p + "ffn_down_weight.bin", (size_t)d * ff / 4);
+        L.down_s = read_bin<float>(p + "ffn_down_scale.bin", d);
+        L.down_b = read_bin<float>(p + "ffn_down_bias.bin", d);
+    }
+    return m;
+}
+
+}  // namespace
+
+// ==================================================================== Impl
+struct GPT2Engine::Impl {
+    GPT2Config cfg{};
+    GPT2EngineOptions opt;
+    hipStream_t stream = nullptr;
+    std::vector<void*> allocs;
+
+    float *wte = nullptr, *wpe = nullptr, *lnf_g = nullptr, *lnf_b = nullptr;
+    struct Layer {
+        float *ln1_g, *ln1_b, *ln2_g, *ln2_b, *qkv_b, *out_b, *up_b, *down_b;
+        QuantWeight qkv, out, up, down;
+    };
+    std::vector<Layer> layers;
+    QuantWeight head{};  // INT8 LM head (quantized wte), optional
+
+    // activations, [max_batch, ...]
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr;
+    float *logits = nullptr;
+    int32_t* act_q = nullptr;
+    float* act_s = nullptr;
+
+    // paged KV cache: per layer [P, bs, H, dh]; row b of the block table maps
+    // its nbps logical blocks to physical blocks b * nbps + i
+    static constexpr int kBlock = 16;
+    int nbps = 0, phys_blocks = 0;
+    size_t layer_elems = 0;
+    char *kc = nullptr, *vc = nullptr;
+    int *block_table = nullptr, *positions = nullptr, *ctx_lens = nullptr, *tokens = nullptr;
+    float* ws = nullptr;
+    size_t ws_bytes = 0;
+
+    int pos = 0;  // host mirror: tokens in every active sequence
+    int* host_tokens = nullptr;  // pinned [max_batch]
+
+    hipGraphExec_t graph = nullptr;
+    int graph_batch = 0;
+
+    template <typename T>
+    T* dev(size_t count) {
+        void* p = nullptr;
+        HIPC(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)));
+        allocs.push_back(p);
+        return static_cast<T*>(p);
+    }
+    template <typename T>
+    T* upload(const std::vector<T>& v) {
+        T* p = dev<T>(v.size());
+        HIPC(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice));
+        return p;
+    }
+    QuantWeight upload_q(const std::vector<int32_t>& w, const std::vector<float>& s, int N, int K) {
+        QuantWeight q;
+        q.packed = upload(w);
+        q.scale = upload(s);
+        q.N = N;
+        q.K = K;
+        return q;
+    }
+
+    void init(const HostModel& m, GPT2EngineOptions o) {
+        cfg = m.cfg;
+        opt = o;
+        if (opt.max_batch < 1 || opt.max_batch > 16) throw std::runtime_error("max_batch must be 1..16");
+        if (opt.kv_dtype != IE_KV_F32 && opt.kv_dtype != IE_KV_BF16) throw std::runtime_error("kv_dtype");
+        HIPC(hipStreamCreate(&stream));
+        const int d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size, B = opt.max_batch;
+        wte = upload(m.wte);
+        wpe = upload(m.wpe);
+        lnf_g = upload(m.lnf_g);
+        lnf_b = upload(m.lnf_b);
+        for (const auto& L : m.layers) {
+            Layer D{};
+            D.ln1_g = upload(L.ln1_g);
+            D.ln1_b = upload(L.ln1_b);
+            D.ln2_g = upload(L.ln2_g);
+            D.ln2_b = upload(L.ln2_b);
+            D.qkv = upload_q(L.qkv_w, L.qkv_s, 3 * d, d);
+            D.qkv_b = upload(L.qkv_b);
+            D.out = upload_q(L.out_w, L.out_s, d, d);
+            D.out_b = upload(L.out_b);
+            D.up = upload_q(L.up_w, L.up_s, ff, d);
+            D.up_b = upload(L.up_b);
+            D.down = upload_q(L.down_w, L.down_s, d, ff);
+            D.down_b = upload(L.down_b);
+            layers.push_back(D);
+        }
+        if (opt.int8_lm_head) {
+            std::vector<int32_t> hw;
+            std::vector<float> hs;
+            quantize_rows_host(m.wte, V, d, hw, hs);
+            head = upload_q(hw, hs, V, d);
+        }
+        x = dev<float>((size_t)B * d);
+        xn = dev<float>((size_t)B * d);
+        qkv = dev<float>((size_t)B * 3 * d);
+        q = dev<float>((size_t)B * d);
+        attn = dev<float>((size_t)B * d);
+        h = dev<float>((size_t)B * ff);
+        logits = dev<float>((size_t)B * V);
+        act_q = dev<int32_t>((size_t)B * std::max(d, ff) / 4);
+        act_s = dev<float>(B);
+
+        nbps = (cfg.max_seq_len + kBlock - 1) / kBlock;
+        phys_blocks = B * nbps;
+        layer_elems = (size_t)phys_blocks * kBlock * d;
+        const size_t esz = opt.kv_dtype == IE_KV_BF16 ? 2 : 4;
+        kc = dev<char>(layer_elems * esz * cfg.n_layers);
+        vc = dev<char>(layer_elems * esz * cfg.n_layers);
+        std::vector<int> table((size_t)B * nbps);
+        std::iota(table.begin(), table.end(), 0);
+        block_table = upload(table);
+        positions = dev<int>(B);
+        ctx_lens = dev<int>(B);
+        tokens = dev<int>(B);
+        const int S = ie_decode_num_splits(cfg.max_seq_len, kBlock, 0);
+        ws_bytes = ie_decode_attn_workspace_bytes(B, cfg.n_heads, cfg.d_head, S);
+        ws = dev<float>(ws_bytes / sizeof(float));
+        HIPC(hipHostMalloc(&host_tokens, sizeof(int) * B));
+        reset();
+    }
+
+    ~Impl() {  // best effort: a destructor has nowhere to report errors
+        if (graph) (void)hipGraphExecDestroy(graph);
+        for (void* p : allocs) (void)hipFree(p);
+        if (host_tokens) (void)hipHostFree(host_tokens);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    void reset() {
+        pos = 0;
+        std::vector<int> z(opt.max_batch, 0);
+        HIPC(hipMemcpyAsync(positions, z.data(), sizeof(int) * z.size(), hipMemcpyHostToDevice, stream));
+        HIPC(hipMemcpyAsync(ctx_lens, z.data(), sizeof(int) * z.size(), hipMemcpyHostToDevice, stream));
+        HIPC(hipStreamSynchronize(stream));
+    }
+
+    void* layer_k(int l) { return kc + layer_elems * (opt.kv_dtype == IE_KV_BF16 ? 2 : 4) * l; }
+    void* layer_v(int l) { return vc + layer_elems * (opt.kv_dtype == IE_KV_BF16 ? 2 : 4) * l; }
+
+    // One decode step for B sequences: reads tokens/positions on the device,
+    // leaves logits, writes the argmax into tokens and advances positions.
+    void enqueue_step(int B) {
+        const int d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size, H = cfg.n_heads;
+        hipStream_t s = stream;
+        ie_stream_t st = (ie_stream_t)s;
+        IEC(ie_embedding_batch(B, tokens, positions, d, wte, wpe, x, st));
+        for (int l = 0; l < cfg.n_layers; ++l) {
+            const Layer& L = layers[l];
+            IEC(ie_layernorm(B, d, x, L.ln1_g, L.ln1_b, xn, 1e-5f, st));
+            IEC(ie_quantize_fp32_to_int8(B, d, xn, act_q, act_s, st));
+            IEC(ie_int8_gemm(B, 3 * d, d, act_q, L.qkv.packed, act_s, L.qkv.scale, IE_EPI_BIAS, L.qkv_b,
+                             nullptr, qkv, st));
+            ie::launch_qkv_split_append(B, d, qkv, positions, block_table, nbps, kBlock, q, layer_k(l),
+                                        layer_v(l), opt.kv_dtype, ctx_lens, s);
+            IEC(ie::check_launch("qkv_split_append"));
+            IEC(ie_decode_attn(B, H, H, cfg.d_head, q, layer_k(l), layer_v(l), opt.kv_dtype,
+                               block_table, ctx_lens, cfg.max_seq_len, kBlock, nbps, attn, ws, ws_bytes, 0,
+                               st));
+            IEC(ie_quantize_fp32_to_int8(B, d, attn, act_q, act_s, st));
+            IEC(ie_int8_gemm(B, d, d, act_q, L.out.packed, act_s, L.out.scale, IE_EPI_BIAS_RESIDUAL,
+                             L.out_b, x, x, st));
+            IEC(ie_layernorm(B, d, x, L.ln2_g, L.ln2_b, xn, 1e-5f, st));
+            IEC(ie_quantize_fp32_to_int8(B, d, xn, act_q, act_s, st));
+            IEC(ie_int8_gemm(B, ff, d, act_q, L.up.packed, act_s, L.up.scale, IE_EPI_BIAS_GELU, L.up_b,
+                             nullptr, h, st));
+            IEC(ie_quantize_fp32_to_int8(B, ff, h, act_q, act_s, st));
+            IEC(ie_int8_gemm(B, d, ff, act_q, L.down.packed, act_s, L.down.scale, IE_EPI_BIAS_RESIDUAL,
+                             L.down_b, x, x, st));
+        }
+        IEC(ie_layernorm(B, d, x, lnf_g, lnf_b, xn, 1e-5f, st));
+        if (opt.int8_lm_head) {
+            IEC(ie_quantize_fp32_to_int8(B, d, xn, act_q, act_s, st));
+            IEC(ie_int8_gemm(B, V, d, act_q, head.packed, act_s, head.scale, IE_EPI_PLAIN, nullptr, nullptr,
+                             logits, st));
+        } else {
+            IEC(ie_vocab_proj(B, xn, wte, logits, d, V, st));
+        }
+        IEC(ie_argmax(B, logits, V, tokens, st));
+        ie::launch_advance(B, positions, s);
+        IEC(ie::check_launch("advance"));
+    }
+
+    void run_step(int B) {
+        if (pos >= cfg.max_seq_len) throw std::runtime_error("context is full (max_seq_len reached)");
+        if (opt.use_graph) {
+            if (!graph || graph_batch != B) {
+                if (graph) HIPC(hipGraphExecDestroy(graph));
+                graph = nullptr;
+                hipGraph_t g;
+                HIPC(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+                try {
+                    enqueue_step(B);
+                } catch (...) {
+                    hipGraph_t dummy = nullptr;
+                    (void)hipStreamEndCapture(stream, &dummy);
+                    if (dummy) (void)hipGraphDestroy(dummy);
+                    throw;
+                }
+                HIPC(hipStreamEndCapture(stream, &g));
+                HIPC(hipGraphInstantiate(&graph, g, nullptr, nullptr, 0));
+                HIPC(hipGraphDestroy(g));
+                graph_batch = B;
+            }
+            HIPC(hipGraphLaunch(graph, stream));
+        } else {
+            enqueue_step(B);
+        }
+        ++pos;
+    }
+
+    // Upload one token per sequence, run a step, fetch the argmax ids.
+    void step_tokens(const int* toks, int B, bool fetch) {
+        std::memcpy(host_tokens, toks, sizeof(int) * B);
+        HIPC(hipMemcpyAsync(tokens, host_tokens, sizeof(int) * B, hipMemcpyHostToDevice, stream));
+        run_step(B);
+        if (fetch) HIPC(hipMemcpyAsync(host_tokens, tokens, sizeof(int) * B, hipMemcpyDeviceToHost, stream));
+        HIPC(hipStreamSynchronize(stream));
+    }
+
+    double bytes_per_step(int B) const {
+        const double d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size;
+        double w = cfg.n_layers * (3 * d * d + d * d + 2 * d * ff);          // int8 weights
+        w += cfg.n_layers * 4.0 * (3 * d + d + ff + d) * 2;                 // scales + biases
+        w += cfg.n_layers * 4.0 * 4 * d;                                      // LayerNorm
+        w += opt.int8_lm_head ? V * d + 4 * V : 4.0 * V * d;                  // LM head
+        const double kv = 2.0 * cfg.n_layers * (double)B * pos * d * (opt.kv_dtype == IE_KV_BF16 ? 2 : 4);
+        return w + kv;
+    }
+
+    void fill_tail_metrics(InferenceMetrics& m, const std::vector<float>& itl, float decode_ms, int B) {
+        const int n = (int)itl.size();
+        if (n > 0) {
+            m.tpot_ms = decode_ms / n;
+            m.tps = 1000.0f * n * B / decode_ms;
+            m.itl_min_ms = *std::min_element(itl.begin(), itl.end());
+            m.itl_max_ms = *std::max_element(itl.begin(), itl.end());
+            auto sorted = itl;
+            std::sort(sorted.begin(), sorted.end());
+            m.itl_p95_ms = n >= 20 ? sorted[(int)(n * 0.95)] : m.itl_max_ms;
+            m.mbu = (float)(bytes_per_step(B) * (1000.0 * n / decode_ms) / 8.0e12);
+        }
+        m.kv_cache_pct = 100.0f * ((pos + kBlock - 1) / kBlock) / nbps;
+        size_t fr = 0, tot = 0;
+        if (hipMemGetInfo(&fr, &tot) == hipSuccess) {
+            m.vram_used_mb = (tot - fr) / (1024.0f * 1024.0f);
+            m.vram_total_mb = tot / (1024.0f * 1024.0f);
+        }
+    }
+};
+
+using Clock = std::chrono::steady_clock;
+static float ms_since(Clock::time_point t) {
+    return std::chrono::duration<float, std::milli>(Clock::now() - t).count();
+}
+
+GPT2Engine::GPT2Engine(const std::string& model_dir, GPT2EngineOptions opt) : impl_(new Impl) {
+    impl_->init(load_model(model_dir), opt);
+}
+
+GPT2Engine::GPT2Engine(const GPT2Config& cfg, uint64_t seed, GPT2EngineOptions opt) : impl_(new Impl) {
+    impl_->init(random_model(cfg, seed), opt);
+}
+
+GPT2Engine::~GPT2Engine() = default;
+
+void GPT2Engine::reset_session() { impl_->reset(); }
+int GPT2Engine::session_tokens() const { return impl_->pos; }
+const GPT2Config& GPT2Engine::config() const { return impl_->cfg; }
+const float* GPT2Engine::logits_device() const { return impl_->logits; }
+double GPT2Engine::step_bytes(int batch) const { return impl_->bytes_per_step(batch); }
+
+void GPT2Engine::step(const int* tokens, int batch) {
+    if (batch < 1 || batch > impl_->opt.max_batch) throw std::runtime_error("batch out of range");
+    impl_->step_tokens(tokens, batch, false);
+}
+
+// src/sampler.cu:16-45: top-k over temperature-scaled softmax, host side.
+static int sample_top_k_host(const std::vector<float>& h, int k, float temperature, std::mt19937& gen) {
+    const int V = (int)h.size();
+    k = std::max(1, std::min(k, V));
+    std::vector<int> idx(V);
+    std::iota(idx.begin(), idx.end(), 0);
+    std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), [&](int a, int b) { return h[a] > h[b]; });
+    std::vector<float> p(k);
+    float sum = 0.0f;
+    for (int i = 0; i < k; ++i) {
+        p[i] = std::exp((h[idx[i]] - h[idx[0]]) / temperature);
+        sum += p[i];
+    }
+    const float r = std::uniform_real_distribution<float>(0.0f, 1.0f)(gen);
+    float cum = 0.0f;
+    for (int i = 0; i < k; ++i) {
+        cum += p[i] / sum;
+        if (r < cum) return idx[i];
+    }
+    return idx[k - 1];
+}
+
+void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tokens, float temperature,
+                          int top_k, bool greedy, std::function<void(int)> token_callback,
+                          InferenceMetrics& metrics, bool reset_kv) {
+    Impl& I = *impl_;
+    metrics = InferenceMetrics{};
+    metrics.max_tokens = max_new_tokens;
+    metrics.generating = true;
+    if (prompt_tokens.empty()) throw std::runtime_error("empty prompt");
+    if (reset_kv) I.reset();
+    std::mt19937 gen(42u);
+    std::vector<float> hl;
+    auto pick = [&]() -> int {
+        if (greedy) return I.host_tokens[0];
+        hl.resize(I.cfg.vocab_size);
+        HIPC(hipMemcpy(hl.data(), I.logits, sizeof(float) * hl.size(), hipMemcpyDeviceToHost));
+        return sample_top_k_host(hl, top_k, temperature, gen);
+    };
+
+    const auto t_total = Clock::now();
+    // Prompt through the decode path, one position per step (what the
+    // reference does for continuation prompts, src/gpt2_engine.cu:680-698).
+    for (size_t i = 0; i < prompt_tokens.size(); ++i)
+        I.step_tokens(&prompt_tokens[i], 1, i + 1 == prompt_tokens.size());
+    int next = pick();
+    metrics.ttft_ms = ms_since(t_total);
+
+    std::vector<float> itl;
+    float decode_ms = 0.0f;
+    for (int stepi = 0; stepi < max_new_tokens; ++stepi) {
+        if (next == 50256) break;  // GPT-2 <|endoftext|>, src/gpt2_engine.cu:717
+        token_callback(next);
+        metrics.tokens_generated = stepi + 1;
+        if (I.pos >= I.cfg.max_seq_len) break;
+        const auto t = Clock::now();
+        I.step_tokens(&next, 1, greedy);
+        next = pick();
+        const float dt = ms_since(t);
+        itl.push_back(dt);
+        decode_ms += dt;
+    }
+    I.fill_tail_metrics(metrics, itl, decode_ms, 1);
+    metrics.end_to_end_ms = ms_since(t_total);
+    metrics.generating = false;
+}
+
+void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, int max_new_tokens,
+                                std::vector<std::vector<int>>& out, InferenceMetrics& metrics,
+                                bool ignore_eos) {
+    Impl& I = *impl_;
+    const int B = (int)prompts.size();
+    if (B < 1 || B > I.opt.max_batch) throw std::runtime_error("batch out of range");
+    const size_t P = prompts[0].size();
+    for (const auto& p : prompts)
+        if (p.size() != P || P == 0) throw std::runtime_error("prompts must share one non-zero length");
+    metrics = InferenceMetrics{};
+    metrics.max_tokens = max_new_tokens;
+    metrics.generating = true;
+    I.reset();
+    out.assign(B, {});
+    std::vector<int> toks(B);
+    const auto t_total = Clock::now();
+    for (size_t i = 0; i < P; ++i) {
+        for (int b = 0; b < B; ++b) toks[b] = prompts[b][i];
+        I.step_tokens(toks.data(), B, i + 1 == P);
+    }
+    metrics.ttft_ms = ms_since(t_total);
+    std::vector<float> itl;
+    float decode_ms = 0.0f;
+    std::vector<char> done(B, 0);
+    for (int stepi = 0; stepi < max_new_tokens; ++stepi) {
+        bool all_done = true;
+        for (int b = 0; b < B; ++b) {
+            const int tkn = I.host_tokens[b];
+            if (!done[b] && !ignore_eos && tkn == 50256) done[b] = 1;
+            if (!done[b]) out[b].push_back(tkn);
+            all_done = all_done && done[b];
+        }
+        metrics.tokens_generated = stepi + 1;
+        if (all_done || stepi + 1 == max_new_tokens || I.pos >= I.cfg.max_seq_len) break;
+        // The argmax of the previous step is already in the device token
+        // buffer: the step reads it directly, only the ids come back.
+        const auto t = Clock::now();
+        I.run_step(B);
+        HIPC(hipMemcpyAsync(I.host_tokens, I.tokens, sizeof(int) * B, hipMemcpyDeviceToHost, I.stream));
+        HIPC(hipStreamSynchronize(I.stream));
+        const float dt = ms_since(t);
+        itl.push_back(dt);
+        decode_ms += dt;
+    }
+    I.fill_tail_metrics(metrics, itl, decode_ms, B);
+    metrics.end_to_end_ms = ms_since(t_total);
+    metrics.generating = false;
+}
+
+void GPT2Engine::write_random_model(const std::string& dir, const GPT2Config& cfg, uint64_t seed) {
+    const HostModel m = random_model(cfg, seed);
+    ::mkdir(dir.c_str(), 0755);
+    {
+        std::ofstream f(dir + "/config.json");
+        f << "{\n  \"n_layers\": " << cfg.n_layers << ",\n  \"n_heads\": " << cfg.n_heads
+          << ",\n  \"d_model\": " << cfg.d_model << ",\n  \"d_ff\": " << cfg.d_ff
+          << ",\n  \"vocab_size\": " << cfg.vocab_size << ",\n  \"max_seq_len\": " << cfg.max_seq_len
+          << ",\n  \"d_head\": " << cfg.d_head << "\n}\n";
+        if (!f) throw std::runtime_error("cannot write config.json");
+    }
+    write_bin(dir + "/wte.bin", m.wte);
+    write_bin(dir + "/wpe.bin", m.wpe);
+    write_bin(dir + "/ln_f_gamma.bin", m.lnf_g);
+    write_bin(dir + "/ln_f_beta.bin", m.lnf_b);
+    for (int i = 0; i < cfg.n_layers; ++i) {
+        char ld[64];
+        std::snprintf(ld, sizeof(ld), "/layer_%02d", i);
+        const std::string p = dir + ld;
+        ::mkdir(p.c_str(), 0755);
+        const auto& L = m.layers[i];
+        write_bin(p + "/ln1_gamma.bin", L.ln1_g);
+        write_bin(p + "/ln1_beta.bin", L.ln1_b);
+        write_bin(p + "/ln2_gamma.bin", L.ln2_g);
+        write_bin(p + "/ln2_beta.bin", L.ln2_b);
+        write_bin(p + "/qkv_weight.bin", L.qkv_w);
+        write_bin(p + "/qkv_scale.bin", L.qkv_s);
+        write_bin(p + "/qkv_bias.bin", L.qkv_b);
+        write_bin(p + "/out_weight.bin", L.out_w);
+        write_bin(p + "/out_scale.bin", L.out_s);
+        write_bin(p + "/out_bias.bin", L.out_b);
+        write_bin(p + "/ffn_up_weight.bin", L.up_w);
+        write_bin(p + "/ffn_up_scale.bin", L.up_s);
+        write_bin(p + "/ffn_up_bias.bin", L.up_b);
+        write_bin(p + "/ffn_down_weight.bin", L.down_w);
+        write_bin(p + "/ffn_down_scale.bin", L.down_s);
+        write_bin(p + "/ffn_down_bias.bin", L.down_b);
+    }
+}

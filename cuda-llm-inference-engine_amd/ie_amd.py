@@ -44,6 +44,32 @@ SIGNATURES = {
     "ie_argmax": (_I, [_I, _P, _I, _P, _P]),
 }
 
+# include/ie_engine.h
+ENGINE_SIGNATURES = {
+    "ie_engine_create": (_I, [ctypes.POINTER(_P), ctypes.c_char_p, _I, _I, _I, _I, _I, _I,
+                              ctypes.c_ulonglong, _I, _I, _I, _I]),
+    "ie_engine_destroy": (_I, [_P]),
+    "ie_engine_write_random_model": (_I, [ctypes.c_char_p, _I, _I, _I, _I, _I, _I, ctypes.c_ulonglong]),
+    "ie_engine_reset": (_I, [_P]),
+    "ie_engine_generate": (_I, [_P, _I, _I, _P, _I, _I, _P, _P]),
+    "ie_engine_step": (_I, [_P, _I, _P, _P, _P]),
+    "ie_engine_session_tokens": (_I, [_P]),
+    "ie_engine_config": (_I, [_P, _P]),
+    "ie_engine_step_bytes": (ctypes.c_double, [_P, _I]),
+}
+
+
+class Metrics(ctypes.Structure):
+    """ie_metrics (include/ie_engine.h): InferenceMetrics without `generating`."""
+    _fields_ = [(n, ctypes.c_float) for n in ("ttft_ms", "tpot_ms", "itl_min_ms", "itl_max_ms",
+                                              "itl_p95_ms", "tps")] + \
+               [("tokens_generated", ctypes.c_int), ("max_tokens", ctypes.c_int)] + \
+               [(n, ctypes.c_float) for n in ("kv_cache_pct", "vram_used_mb", "vram_total_mb", "mbu",
+                                              "end_to_end_ms")]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
 
 class IeError(RuntimeError):
     def __init__(self, fn: str, status: int, msg: str):
@@ -72,7 +98,7 @@ def load() -> ctypes.CDLL:
                 f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
                 "(make -C cuda-llm-inference-engine_amd)")
         lib = ctypes.CDLL(LIB_PATH)
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in list(SIGNATURES.items()) + list(ENGINE_SIGNATURES.items()):
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
@@ -213,3 +239,72 @@ def argmax(logits, out=None, stream=None):
     out = out if out is not None else torch.empty(rows, dtype=torch.int32, device=logits.device)
     check("ie_argmax", rows, _ptr(logits), n, _ptr(out), _stream(stream))
     return out
+
+
+# ---------------------------------------------------------------- engine
+GPT2_SMALL = dict(n_layers=12, n_heads=12, d_model=768, d_ff=3072, vocab_size=50257, max_seq_len=1024)
+
+
+def write_random_model(path, seed=0, **cfg):
+    c = dict(GPT2_SMALL, **cfg)
+    check("ie_engine_write_random_model", str(path).encode(), c["n_layers"], c["n_heads"], c["d_model"],
+          c["d_ff"], c["vocab_size"], c["max_seq_len"], seed)
+
+
+class Engine:
+    """GPT-2 decode engine (include/ie_engine.h).  model_dir=None builds a
+    random model of the given shape (GPT-2 Small by default)."""
+
+    def __init__(self, model_dir=None, seed=0, max_batch=1, kv_dtype=KV_F32, int8_lm_head=False,
+                 use_graph=True, **cfg):
+        import numpy as np  # noqa: F401
+
+        c = dict(GPT2_SMALL, **cfg)
+        h = ctypes.c_void_p()
+        check("ie_engine_create", ctypes.byref(h), None if model_dir is None else str(model_dir).encode(),
+              c["n_layers"], c["n_heads"], c["d_model"], c["d_ff"], c["vocab_size"], c["max_seq_len"], seed,
+              max_batch, kv_dtype, int(int8_lm_head), int(use_graph))
+        self.h = h
+        v = (ctypes.c_int * 7)()
+        check("ie_engine_config", h, ctypes.cast(v, ctypes.c_void_p))
+        self.cfg = dict(zip(("n_layers", "n_heads", "d_model", "d_ff", "vocab_size", "max_seq_len", "d_head"),
+                            list(v)))
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().ie_engine_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def reset(self):
+        check("ie_engine_reset", self.h)
+
+    def step(self, tokens, want_logits=True):
+        import numpy as np
+
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        B = toks.shape[0]
+        V = self.cfg["vocab_size"]
+        logits = np.empty((B, V), dtype=np.float32) if want_logits else None
+        check("ie_engine_step", self.h, B, toks.ctypes.data_as(ctypes.c_void_p),
+              None if logits is None else logits.ctypes.data_as(ctypes.c_void_p), None)
+        return logits
+
+    def generate(self, prompts, max_new, ignore_eos=False):
+        """prompts [B, P] int -> (tokens [B, max_new] with -1 padding, metrics dict)."""
+        import numpy as np
+
+        p = np.ascontiguousarray(prompts, dtype=np.int32)
+        B, P = p.shape
+        out = np.full((B, max_new), -1, dtype=np.int32)
+        m = Metrics()
+        check("ie_engine_generate", self.h, B, P, p.ctypes.data_as(ctypes.c_void_p), max_new, int(ignore_eos),
+              out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(m))
+        return out, m.as_dict()
+
+    def session_tokens(self):
+        return load().ie_engine_session_tokens(self.h)
+
+    def step_bytes(self, batch):
+        return load().ie_engine_step_bytes(self.h, batch)

@@ -11,6 +11,7 @@ import pytest
 from conftest import PKG, ROOT
 
 HDR = os.path.join(ROOT, "include", "ie_amd.h")
+ENGINE_HDR = os.path.join(ROOT, "include", "ie_engine.h")
 COMPAT = os.path.join(ROOT, "include", "ie_compat.h")
 LIB = os.path.join(PKG, "libie_amd.so")
 
@@ -18,9 +19,9 @@ LIB = os.path.join(PKG, "libie_amd.so")
 SIGS_EXPECTED = 16  # entry points declared in include/ie_amd.h
 
 
-def declared_c_functions():
-    text = open(HDR).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t)\s+(ie_\w+)\s*\(", text, re.M)))
+def declared_c_functions(path=HDR):
+    text = open(path).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t|double)\s+(ie_\w+)\s*\(", text, re.M)))
 
 
 def declared_cpp_functions():
@@ -40,8 +41,12 @@ def test_library_loads_and_exports_all(ie):
     lib = ctypes.CDLL(LIB)
     for n in names:
         assert hasattr(lib, n), n
-    # the ctypes table covers exactly the header
+    # the ctypes tables cover exactly the headers
     assert sorted(ie.SIGNATURES) == names
+    eng = declared_c_functions(ENGINE_HDR)
+    assert len(eng) == 9 and sorted(ie.ENGINE_SIGNATURES) == eng
+    for n in eng:
+        assert hasattr(lib, n), n
     syms = exported()
     for n in declared_cpp_functions():
         assert re.search(rf"\b{n}\(", syms), n

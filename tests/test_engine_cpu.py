@@ -1,0 +1,44 @@
+"""Engine host logic without a GPU: the random-model writer produces the
+reference's on-disk format (python/export_gpt2.py:73-167) with per-row int8
+weights, and invalid configurations are rejected with a status code."""
+import json
+import os
+
+import numpy as np
+
+from conftest import unpack_i8
+
+TINY = dict(n_layers=2, n_heads=2, d_model=128, d_ff=256, vocab_size=1000, max_seq_len=64)
+
+
+def test_writer_layout_and_quantization(ie, tmp_path):
+    ie.write_random_model(tmp_path, seed=5, **TINY)
+    cfg = json.load(open(tmp_path / "config.json"))
+    assert cfg == dict(TINY, d_head=64)
+    d, ff, V, S = 128, 256, 1000, 64
+    assert os.path.getsize(tmp_path / "wte.bin") == V * d * 4
+    assert os.path.getsize(tmp_path / "wpe.bin") == S * d * 4
+    for name, N, K in [("qkv", 3 * d, d), ("out", d, d), ("ffn_up", ff, d), ("ffn_down", d, ff)]:
+        w = np.fromfile(tmp_path / "layer_01" / f"{name}_weight.bin", dtype=np.int32).reshape(N, K // 4)
+        s = np.fromfile(tmp_path / "layer_01" / f"{name}_scale.bin", dtype=np.float32)
+        b = np.fromfile(tmp_path / "layer_01" / f"{name}_bias.bin", dtype=np.float32)
+        assert s.shape == (N,) and b.shape == (N,)
+        q = unpack_i8(w).astype(np.int32)
+        assert np.all(np.abs(q).max(axis=1) == 127)          # row max maps to +-127
+        deq = q * s[:, None]
+        assert 0.015 < deq.std() < 0.025                      # N(0, 0.02) weights
+        assert np.all(s > 0) and np.allclose(s, np.abs(deq).max(axis=1) / 127, rtol=1e-6)
+    g = np.fromfile(tmp_path / "layer_00" / "ln1_gamma.bin", dtype=np.float32)
+    assert np.all(g == 1.0)
+    # same seed, same bytes
+    other = tmp_path / "again"
+    ie.write_random_model(other, seed=5, **TINY)
+    assert open(tmp_path / "layer_00" / "qkv_weight.bin", "rb").read() == \
+        open(other / "layer_00" / "qkv_weight.bin", "rb").read()
+
+
+def test_writer_rejects_bad_config(ie, tmp_path):
+    st = ie.call("ie_engine_write_random_model", str(tmp_path / "x").encode(), 2, 3, 128, 256, 100, 64, 1)
+    assert st == ie.IE_ERR_INVALID  # d_head = 128 / 3 is not an integer head size
+    st = ie.call("ie_engine_write_random_model", str(tmp_path / "y").encode(), 2, 4, 128, 256, 100, 64, 1)
+    assert st == ie.IE_ERR_INVALID and "d_head" in ie.last_error()  # d_head 32 unsupported
