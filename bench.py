@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip", default="", help="comma list of gemv,gemm512,attn,cpu,e2e")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE passes")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
 
 
@@ -258,6 +260,116 @@ def bench_attn(ie):
     return out
 
 
+# ------------------------------------------------------------------ end to end
+def bench_e2e(ie):
+    """GPT-2 Small random-init N(0, 0.02), INT8 per-row
+    linears (W8A8 as the reference engine), paged KV, prompt of 128 random ids,
+    greedy decode of 256 tokens at batch 1 and 16.  tok/s counts decode steps
+    only (src/gpt2_engine.cu:754); MBU = bytes streamed per step x steps/s / 8 TB/s."""
+    import numpy as np
+
+    out = []
+    rng = np.random.default_rng(128)
+    for head_i8 in (False, True):
+        eng = ie.Engine(None, seed=1234, max_batch=16, int8_lm_head=head_i8)
+        for B in (1, 16):
+            prompts = rng.integers(0, 50257, (B, 128)).astype(np.int32)
+            eng.generate(prompts, 8, ignore_eos=True)  # warm up (graph capture)
+            toks, m = eng.generate(prompts, 256, ignore_eos=True)
+            r = {"batch": B, "lm_head": "int8" if head_i8 else "fp32 (reference)",
+                 "decode_tok_s": round(m["tps"], 1), "tpot_ms": round(m["tpot_ms"], 4),
+                 "ttft_ms": round(m["ttft_ms"], 2), "itl_p95_ms": round(m["itl_p95_ms"], 4),
+                 "mbu": round(m["mbu"], 4), "tokens": int((toks >= 0).sum())}
+            out.append(r)
+            log(f"e2e {r}")
+        eng.close()
+    return out
+
+
+# ------------------------------------------------------------------ HBM traffic
+CALIB_BYTES = 1 << 30
+TRAFFIC_KERNELS = {"gemm": "gemm_i8_256_kernel", "gemv": "gemv_i8_fixed_kernel",
+                   "attn": "decode_attn_split_kernel"}
+
+
+def pmc_child(ie):
+    """Workload profiled by the FETCH_SIZE / WRITE_SIZE passes: a 1 GiB device
+    copy (calibration: known bytes each way), then one launch of each dominant
+    kernel on its bench shape."""
+    import torch
+
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    h = bench_headline(ie, 2, 1)
+    del h
+    g = torch.Generator(device="cuda").manual_seed(9)
+    K, N = 8192, 28672
+    W = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
+    A = torch.randint(-127, 128, (1, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
+    sA = torch.ones(1, device="cuda")
+    sB = torch.ones(N, device="cuda")
+    ie.int8_gemm(A, W, sA, sB, ie.EPI_PLAIN)
+    torch.cuda.synchronize()
+    del W
+    attn_case(ie, 32, 32, 8, 128, 8192, False, False, 8192)
+    torch.cuda.synchronize()
+
+
+def measure_traffic():
+    """Runs the PMC passes in child processes; returns per-kernel HBM bytes per
+    launch (FETCH_SIZE + WRITE_SIZE, KiB, scaled by what the counters read for
+    the calibration copy) or None if rocprofv3 is unavailable."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    if shutil.which("rocprofv3") is None:
+        return None
+    out = {}
+    with tempfile.TemporaryDirectory(dir="/tmp") as td:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = os.path.join(td, counter)
+            cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv",
+                   "-d", d, "-o", "run", "--", sys.executable, os.path.abspath(__file__), "--pmc-child"]
+            r = subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), capture_output=True,
+                               text=True)
+            files = [os.path.join(dp, f) for dp, _, fs in os.walk(d) for f in fs
+                     if f.endswith("counter_collection.csv")]
+            if r.returncode != 0 and not files:
+                log(f"traffic pass {counter} failed rc={r.returncode}: {r.stderr[-500:]}")
+                return None
+            vals = {}
+            for row in csv.DictReader(open(files[0])):
+                if row["Counter_Name"] != counter:
+                    continue
+                name = row["Kernel_Name"]
+                key = "copy" if "copy" in name.lower() or "elementwise_kernel" in name else None
+                for k, pat in TRAFFIC_KERNELS.items():
+                    if pat in name:
+                        key = k
+                if key:
+                    vals.setdefault(key, []).append(float(row["Counter_Value"]) * 1024.0)
+            for k, v in vals.items():
+                # the calibration copy is the largest "copy"-like dispatch
+                out.setdefault(k, {})[counter] = max(v) if k == "copy" else sum(v) / len(v)
+    cp = out.get("copy", {})
+    if not cp.get("FETCH_SIZE") or not cp.get("WRITE_SIZE"):
+        return None
+    f_scale = CALIB_BYTES / cp["FETCH_SIZE"]
+    w_scale = CALIB_BYTES / cp["WRITE_SIZE"]
+    res = {"calibration": {"copy_bytes": CALIB_BYTES, "fetch_factor": round(f_scale, 4),
+                           "write_factor": round(w_scale, 4)}}
+    for k in TRAFFIC_KERNELS:
+        if k in out and "FETCH_SIZE" in out[k] and "WRITE_SIZE" in out[k]:
+            res[k] = {"fetch_bytes": int(out[k]["FETCH_SIZE"] * f_scale),
+                      "write_bytes": int(out[k]["WRITE_SIZE"] * w_scale)}
+    return res
+
+
 # ------------------------------------------------------------------ CPU baseline
 def cpu_baseline(inputs, budget_s=12.0):
     import numpy as np
@@ -291,6 +403,12 @@ def cpu_baseline(inputs, budget_s=12.0):
 
 def main():
     args = parse()
+    if args.pmc_child:
+        import ie_amd as ie
+
+        ie.load()
+        pmc_child(ie)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(this build runs on a single MI355X)", file=sys.stderr)
@@ -325,10 +443,9 @@ def main():
     if not args.only_headline:
         if "gemv" not in skip:
             res["gemv"] = bench_gemv(ie)
-            big = [r for r in res["gemv"] if r["N"] * r["K"] >= 768 * 50257]
-            best = max(big, key=lambda r: r["GBps"])
-            res["gemv_roofline"] = roof(best["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
-            res["gemv_roofline"]["kernel"] = f"gemv M={best['M']} K={best['K']} N={best['N']}"
+            dom = [r for r in res["gemv"] if (r["M"], r["K"], r["N"]) == (1, 8192, 28672)][0]
+            res["gemv_roofline"] = roof(dom["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
+            res["gemv_roofline"]["kernel"] = "gemv M=1 K=8192 N=28672 (decode GEMV, 235 MB of weights)"
         if "gemm512" not in skip:
             res["gemm_m512"] = bench_gemm512(ie)
         if "attn" not in skip:
@@ -336,9 +453,21 @@ def main():
             c8 = [r for r in res["decode_attn"] if r["ctx"] == 8192 and r["kv"] == "fp32"][0]
             res["decode_attn_roofline"] = roof(c8["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
             res["decode_attn_roofline"]["kernel"] = "decode_attn cfg4 ctx 8192 fp32"
+        if "e2e" not in skip:
+            res["e2e_gpt2"] = bench_e2e(ie)
     if "cpu" not in skip:
         log("cpu baseline")
         res["cpu_baseline"] = cpu_baseline(h["inputs"])
+    if not args.no_traffic:
+        log("traffic (rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
+        t = measure_traffic()
+        res["traffic_detail"] = t
+        if t and "gemm" in t:
+            res["roofline"]["traffic"] = t["gemm"]["fetch_bytes"] + t["gemm"]["write_bytes"]
+        if t and "gemv" in t and "gemv_roofline" in res:
+            res["gemv_roofline"]["traffic"] = t["gemv"]["fetch_bytes"] + t["gemv"]["write_bytes"]
+        if t and "attn" in t and "decode_attn_roofline" in res:
+            res["decode_attn_roofline"]["traffic"] = t["attn"]["fetch_bytes"] + t["attn"]["write_bytes"]
     print(json.dumps(res), flush=True)
 
 
