@@ -270,13 +270,16 @@ def bench_e2e(ie):
 
     out = []
     rng = np.random.default_rng(128)
-    for head_i8 in (False, True):
-        eng = ie.Engine(None, seed=1234, max_batch=16, int8_lm_head=head_i8)
+    # fused step (5 launches per layer) for both LM heads; the unfused step
+    # (every operation through the public C ABI) for comparison
+    for head_i8, fuse in ((False, True), (True, True), (False, False)):
+        eng = ie.Engine(None, seed=1234, max_batch=16, int8_lm_head=head_i8, fuse=fuse)
         for B in (1, 16):
             prompts = rng.integers(0, 50257, (B, 128)).astype(np.int32)
             eng.generate(prompts, 8, ignore_eos=True)  # warm up (graph capture)
             toks, m = eng.generate(prompts, 256, ignore_eos=True)
             r = {"batch": B, "lm_head": "int8" if head_i8 else "fp32 (reference)",
+                 "step": "fused" if fuse else "unfused",
                  "decode_tok_s": round(m["tps"], 1), "tpot_ms": round(m["tpot_ms"], 4),
                  "ttft_ms": round(m["ttft_ms"], 2), "itl_p95_ms": round(m["itl_p95_ms"], 4),
                  "mbu": round(m["mbu"], 4), "tokens": int((toks >= 0).sum())}

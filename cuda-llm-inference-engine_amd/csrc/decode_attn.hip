@@ -22,7 +22,10 @@
 //     hardware exp2; partials store m in that base-2 domain;
 //   * every split writes its slot, empty ones as (o=0, m=-inf, l=0), so the
 //     merge never reads stale workspace (the reference skips the write).
-// Pass 2 (one wave per (b, query head)) merges the splits with l > 0.
+// Pass 2 (one wave per (b, query head)) merges the splits with l > 0.  (A
+// "last split to arrive merges" variant needs a device-scope release per
+// workgroup, which on gfx950 writes back the XCD's L2 and cost more than the
+// second launch.)
 #include <cmath>
 
 #include "device_util.h"
@@ -146,6 +149,64 @@ __device__ __forceinline__ void consume_chunk(const Chunk<D, KV>& c, const float
     }
 }
 
+// Merges the S split partials (o[D], m, l) of one (b, query head) with one
+// wave: lanes read the (m, l) of 64 splits at a time in parallel, and the
+// o rows are accumulated with loads that do not depend on each other, so the
+// merge costs a few memory round trips rather than one per split.  Empty
+// splits hold (0, -inf, 0) and get weight 0.
+template <int D>
+__device__ __forceinline__ void merge_head(const float* __restrict__ w, int S,
+                                           float* __restrict__ out, int lane) {
+    constexpr int PER = D / 64;
+    float mx = -INFINITY;
+    for (int s0 = 0; s0 < S; s0 += 64) {
+        const int s = s0 + lane;
+        if (s < S) {
+            const float* p = w + (size_t)s * (D + 2);
+            if (p[D + 1] > 0.0f) mx = fmaxf(mx, p[D]);
+        }
+    }
+    mx = wave_max(mx);
+    float o[PER], l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) o[i] = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += 64) {
+        const int s = s0 + lane;
+        float f = 0.0f;
+        if (s < S) {
+            const float* p = w + (size_t)s * (D + 2);
+            const float ls = p[D + 1];
+            f = ls > 0.0f ? exp2f(p[D] - mx) : 0.0f;
+            l = fmaf(ls, f, l);
+        }
+        const int cnt = min(64, S - s0);
+        const float* p0 = w + (size_t)s0 * (D + 2) + lane;
+        for (int jb = 0; jb < cnt; jb += 8) {
+            // Eight splits' o rows in flight; indices past cnt re-read the
+            // last one and are masked.
+            float pv[8][PER];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int j = min(jb + u, cnt - 1);
+#pragma unroll
+                for (int i = 0; i < PER; ++i) pv[u][i] = p0[(size_t)j * (D + 2) + 64 * i];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float fj = __shfl(f, (jb + u) & 63, 64);
+                if (jb + u < cnt) {
+#pragma unroll
+                    for (int i = 0; i < PER; ++i) o[i] = fmaf(pv[u][i], fj, o[i]);
+                }
+            }
+        }
+    }
+    l = wave_sum(l);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) out[lane + 64 * i] = o[i] * inv;
+}
+
 template <int D, int G, typename KV>
 __global__ __launch_bounds__(256) void decode_attn_split_kernel(
     const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
@@ -260,32 +321,10 @@ template <int D>
 __global__ __launch_bounds__(256) void decode_attn_merge_kernel(int BH, int num_splits,
                                                                 const float* __restrict__ ws,
                                                                 float* __restrict__ O) {
-    constexpr int PER = D / 64;
     const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (bh >= BH) return;
-    const int lane = threadIdx.x & 63;
-    const float* w = ws + (size_t)bh * num_splits * (D + 2);
-    float mx = -INFINITY;
-    for (int s = 0; s < num_splits; ++s) {
-        const float* p = w + (size_t)s * (D + 2);
-        if (p[D + 1] > 0.0f) mx = fmaxf(mx, p[D]);
-    }
-    float o[PER], l = 0.0f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) o[i] = 0.0f;
-    for (int s = 0; s < num_splits; ++s) {
-        const float* p = w + (size_t)s * (D + 2);
-        const float ls = p[D + 1];
-        if (ls > 0.0f) {
-            const float f = exp2f(p[D] - mx);
-            l = fmaf(ls, f, l);
-#pragma unroll
-            for (int i = 0; i < PER; ++i) o[i] = fmaf(p[lane + 64 * i], f, o[i]);
-        }
-    }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) O[(size_t)bh * D + lane + 64 * i] = o[i] * inv;
+    merge_head<D>(ws + (size_t)bh * num_splits * (D + 2), num_splits, O + (size_t)bh * D,
+                  threadIdx.x & 63);
 }
 
 template <int D, int G, typename KV>

@@ -68,6 +68,53 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// The per-row symmetric quantizer's arithmetic (kernels/quantization/
+// 14_int8_gemm.cu:37-51 of the reference): scale = row_max / 127 (1 for an
+// all-zero row), byte = clamp(rint(x * (1 / scale)), -128, 127).  Shared by
+// the standalone quantizer and the GEMV prologues, so both give identical
+// bytes for the same row.
+__device__ __forceinline__ float quant_scale(float row_max) {
+    return row_max > 0.0f ? row_max / 127.0f : 1.0f;
+}
+__device__ __forceinline__ uint32_t quant_byte(float x, float inv) {
+    const float r = fminf(fmaxf(rintf(x * inv), -128.0f), 127.0f);
+    return (uint32_t)((int32_t)r) & 0xffu;
+}
+__device__ __forceinline__ int32_t quant_word(float4 v, float inv) {
+    return (int32_t)(quant_byte(v.x, inv) | (quant_byte(v.y, inv) << 8) |
+                     (quant_byte(v.z, inv) << 16) | (quant_byte(v.w, inv) << 24));
+}
+
+// LayerNorm of one row held by one wave (kernels/layernorm/
+// 15_layernorm_residual.cu:59-103 of the reference: mean = E[x],
+// var = E[x^2] - mean^2, y = gamma (x - mean) rsqrt(var + eps) + beta).
+// Lane l accumulates its float4s l, l + 64, ... in index order (x, y, z, w),
+// then the wave combines the partials in a fixed butterfly.  The standalone
+// LayerNorm and the GEMV prologue both use these, so they give identical
+// bits for the same row.
+__device__ __forceinline__ void ln_accum(float4 v, float& s, float& s2) {
+    s += v.x;
+    s += v.y;
+    s += v.z;
+    s += v.w;
+    s2 = fmaf(v.x, v.x, s2);
+    s2 = fmaf(v.y, v.y, s2);
+    s2 = fmaf(v.z, v.z, s2);
+    s2 = fmaf(v.w, v.w, s2);
+}
+__device__ __forceinline__ void ln_finish(float s, float s2, int cols, float eps, float& mean,
+                                          float& rs) {
+    s = wave_sum(s);
+    s2 = wave_sum(s2);
+    mean = s / (float)cols;
+    const float var = fmaf(-mean, mean, s2 / (float)cols);
+    rs = rsqrtf(var + eps);
+}
+__device__ __forceinline__ float4 ln_apply(float4 v, float4 g, float4 b, float mean, float rs) {
+    return make_float4(fmaf(g.x * (v.x - mean), rs, b.x), fmaf(g.y * (v.y - mean), rs, b.y),
+                       fmaf(g.z * (v.z - mean), rs, b.z), fmaf(g.w * (v.w - mean), rs, b.w));
+}
+
 // 8-bit signed dot product accumulate: acc + sum_i a.byte[i] * b.byte[i].
 __device__ __forceinline__ int32_t dot4_i8(int32_t a, int32_t b, int32_t acc) {
     return __builtin_amdgcn_sdot4(a, b, acc, false);

@@ -28,12 +28,89 @@ namespace {
 constexpr int kRowsPerWG = 16;
 constexpr int kChunk = 128;  // 16-byte columns of A per LDS chunk (2 KiB of K)
 
+// Output store of every GEMV kernel: the GEMM epilogues, or (kEpiQKV) the
+// bias epilogue routed as the reference's qkv_split + kv_cache_write
+// (src/gpt2_engine.cu:292-315, 321-346) would place it.
+template <int EPI>
+__device__ __forceinline__ void gemv_store(void* C, int m, int n, int N, int32_t acc, float sa,
+                                           float sb, const float* bias, const float* residual,
+                                           const GemvFusion& f) {
+    if constexpr (EPI == kEpiQKV) {
+        const float v = fmaf((float)acc * sa, sb, bias[n]);
+        const int d = N / 3;
+        const int pos = f.positions[m];
+        if (n < d) {
+            f.q[(size_t)m * d + n] = v;
+            if (n == 0) f.ctx_lens[m] = pos + 1;
+        } else {
+            const int blk = pos / f.block_size;
+            const size_t slot = (size_t)f.table[(size_t)m * f.nbps + blk] * f.block_size +
+                                (pos - blk * f.block_size);
+            const bool is_k = n < 2 * d;
+            const size_t i = slot * d + (is_k ? n - d : n - 2 * d);
+            void* base = is_k ? f.kc : f.vc;
+            if (f.kv_dtype == IE_KV_BF16)
+                static_cast<uint16_t*>(base)[i] = f32_to_bf16_rne(v);
+            else
+                static_cast<float*>(base)[i] = v;
+        }
+    } else {
+        store_epilogue<EPI>(C, (size_t)m * N + n, acc, sa, sb, bias, residual, n);
+    }
+}
+
+// One wave builds one int8 activation row of K bytes in LDS (K / 4 words at
+// dst) from fp32 row xr: optionally LayerNorm (ln_* as the standalone
+// LayerNorm), then the per-row quantizer (quant_scale / quant_word, as
+// quant.hip).  So the bytes equal those of the standalone LayerNorm +
+// quantizer pair, and do not depend on M or on which kernel stages the row.
+template <int K, int SRC>
+__device__ __forceinline__ void stage_row(const float* __restrict__ xr, const GemvFusion& f,
+                                          int32_t* dst, float* scale, int lane) {
+    static_assert(K % 256 == 0, "a lane stages whole float4s");
+    constexpr int NV = K / 256;
+    float4 v[NV];
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = x4[lane + 64 * i];
+    if constexpr (SRC == kSrcLnQuant) {
+        float s = 0.0f, s2 = 0.0f, mean, rs;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) ln_accum(v[i], s, s2);
+        ln_finish(s, s2, K, f.eps, mean, rs);
+        const float4* g4 = reinterpret_cast<const float4*>(f.gamma);
+        const float4* b4 = reinterpret_cast<const float4*>(f.beta);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] = ln_apply(v[i], g4[lane + 64 * i], b4[lane + 64 * i], mean, rs);
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
+                             fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    mx = wave_max(mx);
+    const float sc = quant_scale(mx);
+    const float inv = 1.0f / sc;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) dst[lane + 64 * i] = quant_word(v[i], inv);
+    if (lane == 0) *scale = sc;
+}
+
+// Rows m >= M of a fused prologue: zero bytes (their outputs are not stored).
+template <int K>
+__device__ __forceinline__ void zero_row(int32_t* dst, float* scale, int lane) {
+#pragma unroll
+    for (int i = 0; i < K / 256; ++i) dst[lane + 64 * i] = 0;
+    if (lane == 0) *scale = 0.0f;
+}
+
 // Shared tail: reduce each row's 16 lane partials with DPP and store.
 template <int MT, int EPI>
 __device__ __forceinline__ void gemv_finish(const int32_t (&acc)[MT], int li, int n, bool row_ok,
-                                            int M, int N, const float* __restrict__ sA,
+                                            int M, int N, const float* sA,
                                             const float* __restrict__ sB, const float* bias,
-                                            const float* residual, void* C) {
+                                            const float* residual, void* C,
+                                            const GemvFusion& f) {
     int32_t mine = 0;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -41,13 +118,12 @@ __device__ __forceinline__ void gemv_finish(const int32_t (&acc)[MT], int li, in
         if (li == m) mine = t;
     }
     if (row_ok && li < M) {
-        const size_t idx = (size_t)li * N + n;
         float sa = 0.0f, sb = 0.0f;
         if constexpr (EPI != IE_EPI_I32) {
             sa = sA[li];
             sb = sB[n];
         }
-        store_epilogue<EPI>(C, idx, mine, sa, sb, bias, residual, n);
+        gemv_store<EPI>(C, li, n, N, mine, sa, sb, bias, residual, f);
     }
 }
 
@@ -73,15 +149,20 @@ __device__ __forceinline__ void dot_chunk(int32_t (&acc)[MT], const i32x4 wv, co
 // keeps 12-24 16-byte HBM reads in flight.  The first group's loads are issued
 // before the activation block A[M, K] is staged in LDS, so the staging
 // latency hides behind them.
-template <int MT, int EPI, int K16>
+//
+// With SRC != kSrcInt8 wave w builds activation row w itself (stage_row) while
+// the first weight loads are in flight, and the row scales come from LDS.
+template <int MT, int EPI, int K16, int SRC = kSrcInt8>
 __global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
     int M, int N, const int32_t* __restrict__ A, const int32_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
-    const float* residual, void* C) {
+    const float* residual, void* C, GemvFusion f) {
     constexpr int CPL = K16 / 16;                             // chunks per lane per row
     constexpr int G = CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;   // row groups per pass
     static_assert(CPL <= 32, "fixed-K GEMV covers K <= 8192");
+    static_assert(SRC == kSrcInt8 || MT <= 4, "one staging wave per row");
     __shared__ i32x4 a_lds[MT * K16];
+    __shared__ float s_sa[MT];
     const int lane = threadIdx.x & 63;
     const int li = lane & 15;
     const int wave_global = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -101,13 +182,25 @@ __global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
     int r0 = wave_global * (4 * G);
     if (r0 < N) load_group(r0);
 
-    const i32x4* a4 = reinterpret_cast<const i32x4*>(A);
-    for (int i = threadIdx.x; i < MT * K16; i += 256) {
-        const int m = i / K16;
-        const int mm = m < M ? m : M - 1;
-        a_lds[i] = a4[(size_t)mm * K16 + (i - m * K16)];
+    if constexpr (SRC == kSrcInt8) {
+        const i32x4* a4 = reinterpret_cast<const i32x4*>(A);
+        for (int i = threadIdx.x; i < MT * K16; i += 256) {
+            const int m = i / K16;
+            const int mm = m < M ? m : M - 1;
+            a_lds[i] = a4[(size_t)mm * K16 + (i - m * K16)];
+        }
+    } else {
+        const int w = threadIdx.x >> 6;
+        if (w < MT) {
+            int32_t* dst = reinterpret_cast<int32_t*>(a_lds + w * K16);
+            if (w < M)
+                stage_row<K16 * 16, SRC>(f.x + (size_t)w * K16 * 16, f, dst, &s_sa[w], lane);
+            else
+                zero_row<K16 * 16>(dst, &s_sa[w], lane);
+        }
     }
     __syncthreads();
+    const float* sa_src = SRC == kSrcInt8 ? sA : s_sa;
 
     for (; r0 < N; r0 += step) {
         if constexpr (CPL > 16)
@@ -128,7 +221,7 @@ __global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int n = r0 + g * 4 + (lane >> 4);
-            gemv_finish<MT, EPI>(acc[g], li, n, n < N, M, N, sA, sB, bias, residual, C);
+            gemv_finish<MT, EPI>(acc[g], li, n, n < N, M, N, sa_src, sB, bias, residual, C, f);
         }
     }
 }
@@ -168,7 +261,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
             for (int c = li; c < cw; c += 16) dot_chunk<MT>(acc, w[c0 + c], a_lds, kChunk, c);
         }
     }
-    gemv_finish<MT, EPI>(acc, li, n, row_ok, M, N, sA, sB, bias, residual, C);
+    gemv_finish<MT, EPI>(acc, li, n, row_ok, M, N, sA, sB, bias, residual, C, GemvFusion{});
 }
 
 // 5 <= M <= 16: v_mfma_i32_16x16x64_i8 with the activations (M padded to 16
@@ -178,20 +271,33 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
 // MFMA streams 1 KiB of weights; dot4 would need 4 instructions per weight
 // byte at M = 16, which caps it below HBM speed.  Accumulator v of lane l is
 // C[4 * (l / 16) + v][n0 + l % 16].
-template <int EPI, int K64>
+// With SRC != kSrcInt8 wave w builds activation rows w, w + 4, ... itself.
+template <int EPI, int K64, int SRC = kSrcInt8>
 __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
     int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
-    const float* residual, void* C) {
+    const float* residual, void* C, GemvFusion f) {
     constexpr int K = K64 * 64;
     constexpr int U = K64 % 8 == 0 ? 8 : (K64 % 4 == 0 ? 4 : 2);  // loads in flight per lane
     __shared__ i32x4 a_lds[16 * K / 16];
-    for (int i = threadIdx.x; i < 16 * (K / 16); i += 256) {
-        const int m = i / (K / 16);
-        const int mm = m < M ? m : M - 1;
-        a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)mm * K)[i - m * (K / 16)];
+    __shared__ float s_sa[16];
+    if constexpr (SRC == kSrcInt8) {
+        for (int i = threadIdx.x; i < 16 * (K / 16); i += 256) {
+            const int m = i / (K / 16);
+            const int mm = m < M ? m : M - 1;
+            a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)mm * K)[i - m * (K / 16)];
+        }
+    } else {
+        for (int m = threadIdx.x >> 6; m < 16; m += 4) {
+            int32_t* dst = reinterpret_cast<int32_t*>(a_lds + m * (K / 16));
+            if (m < M)
+                stage_row<K, SRC>(f.x + (size_t)m * K, f, dst, &s_sa[m], threadIdx.x & 63);
+            else
+                zero_row<K>(dst, &s_sa[m], threadIdx.x & 63);
+        }
     }
     __syncthreads();
+    const float* sa_src = SRC == kSrcInt8 ? sA : s_sa;
     const int lane = threadIdx.x & 63;
     const int col = lane & 15, kq = lane >> 4;
     const int wave_global = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -224,8 +330,8 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
                 const int m = 4 * kq + v;
                 if (m < M) {
                     float sa = 0.0f;
-                    if constexpr (EPI != IE_EPI_I32) sa = sA[m];
-                    store_epilogue<EPI>(C, (size_t)m * N + n, acc[v], sa, sb, bias, residual, n);
+                    if constexpr (EPI != IE_EPI_I32) sa = sa_src[m];
+                    gemv_store<EPI>(C, m, n, N, acc[v], sa, sb, bias, residual, f);
                 }
             }
         }
@@ -256,22 +362,30 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
     store_epilogue<EPI>(C, idx, s, sa, sb, bias, residual, n);
 }
 
-template <int MT, int EPI, int K16>
-void launch_fixed(const GemmArgs& a, hipStream_t s) {
+template <int MT, int EPI, int K16, int SRC = kSrcInt8>
+void launch_fixed(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFusion{}) {
     constexpr int CPL = K16 / 16;
     constexpr int G = CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;
     const int rows_per_wg = 4 * 4 * G;
     const unsigned blocks = (unsigned)min((a.N + rows_per_wg - 1) / rows_per_wg, 2048);
-    gemv_i8_fixed_kernel<MT, EPI, K16><<<blocks, 256, 0, s>>>(a.M, a.N, a.A, a.BT, a.sA, a.sB,
-                                                              a.bias, a.residual, a.C);
+    gemv_i8_fixed_kernel<MT, EPI, K16, SRC><<<blocks, 256, 0, s>>>(
+        a.M, a.N, a.A, a.BT, a.sA, a.sB, a.bias, a.residual, a.C, f);
 }
 
-template <int EPI, int K64>
-void launch_mfma16(const GemmArgs& a, hipStream_t s) {
+template <int EPI, int K64, int SRC = kSrcInt8>
+void launch_mfma16(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFusion{}) {
     const unsigned blocks = (unsigned)min((a.N + 63) / 64, 2048);
-    gemv_i8_mfma16_kernel<EPI, K64><<<blocks, 256, 0, s>>>(
+    gemv_i8_mfma16_kernel<EPI, K64, SRC><<<blocks, 256, 0, s>>>(
         a.M, a.N, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
-        a.sA, a.sB, a.bias, a.residual, a.C);
+        a.sA, a.sB, a.bias, a.residual, a.C, f);
+}
+
+template <int EPI, int K, int SRC>
+void launch_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s) {
+    if (a.M <= 1) launch_fixed<1, EPI, K / 16, SRC>(a, s, f);
+    else if (a.M <= 2) launch_fixed<2, EPI, K / 16, SRC>(a, s, f);
+    else if (a.M <= 4) launch_fixed<4, EPI, K / 16, SRC>(a, s, f);
+    else launch_mfma16<EPI, K / 64, SRC>(a, s, f);
 }
 
 template <int MT, int EPI>
@@ -325,6 +439,29 @@ void launch_gemv_i8(const GemmArgs& a, hipStream_t s) {
         dispatch_epilogue<GemvLaunch>(a.epi, a, s);
     else
         dispatch_epilogue<GenericLaunch>(a.epi, a, s);
+}
+
+// The decode step's combinations at the GPT-2 widths: LayerNorm-fed QKV
+// (append epilogue), FFN-up (GELU) and INT8 LM head (plain) at K = d = 768;
+// quantizer-fed attention-out (K = 768) and FFN-down (K = 3072) with the
+// residual epilogue.
+bool gemv_fused_supported(int M, int K, int src, int epi) {
+    if (M < 1 || M > kGemvMaxM) return false;
+    if (src == kSrcLnQuant)
+        return K == 768 && (epi == kEpiQKV || epi == IE_EPI_BIAS_GELU || epi == IE_EPI_PLAIN);
+    if (src == kSrcQuant) return (K == 768 || K == 3072) && epi == IE_EPI_BIAS_RESIDUAL;
+    return false;
+}
+
+void launch_gemv_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s) {
+    if (a.M == 0 || a.N == 0) return;
+    if (f.src == kSrcLnQuant) {
+        if (a.epi == kEpiQKV) return launch_fused<kEpiQKV, 768, kSrcLnQuant>(a, f, s);
+        if (a.epi == IE_EPI_BIAS_GELU) return launch_fused<IE_EPI_BIAS_GELU, 768, kSrcLnQuant>(a, f, s);
+        return launch_fused<IE_EPI_PLAIN, 768, kSrcLnQuant>(a, f, s);
+    }
+    if (a.K == 768) return launch_fused<IE_EPI_BIAS_RESIDUAL, 768, kSrcQuant>(a, f, s);
+    launch_fused<IE_EPI_BIAS_RESIDUAL, 3072, kSrcQuant>(a, f, s);
 }
 
 // Used by the MFMA path for shapes its vector loads cannot cover.

@@ -34,6 +34,36 @@ struct GemmArgs {
 };
 // dot4 GEMV for small M (gemv_i8.hip); M in [1, 16].
 void launch_gemv_i8(const GemmArgs& a, hipStream_t s);
+
+// Decode-step fusions of the small-M GEMV (gemv_i8.hip), used by the engine.
+// The activation operand is built inside the GEMV from fp32 rows instead of
+// being read as int8 (src 1: the per-row quantizer of quant.hip, same
+// arithmetic; src 2: LayerNorm first), and the QKV epilogue writes Q and
+// appends K/V to the paged cache instead of storing [M, 3d].
+enum { kSrcInt8 = 0, kSrcQuant = 1, kSrcLnQuant = 2 };
+constexpr int kEpiQKV = 8;  // bias epilogue routed to Q / K cache / V cache
+struct GemvFusion {
+    int src = kSrcInt8;
+    const float* x = nullptr;      // [M, K] fp32 rows (src 1, 2)
+    const float* gamma = nullptr;  // LayerNorm weight and bias [K] (src 2)
+    const float* beta = nullptr;
+    float eps = 1e-5f;
+    // kEpiQKV: N = 3d; Q [M, d]; K/V of token positions[m] of sequence m go
+    // to slot table[m * nbps + pos / block_size] * block_size + pos % block_size
+    // of the [slots, d] caches; ctx_lens[m] = pos + 1.
+    float* q = nullptr;
+    void* kc = nullptr;
+    void* vc = nullptr;
+    int kv_dtype = IE_KV_F32;
+    const int* positions = nullptr;
+    const int* table = nullptr;
+    int nbps = 0;
+    int block_size = 16;
+    int* ctx_lens = nullptr;
+};
+// Whether launch_gemv_fused has a kernel for this combination (M <= 16).
+bool gemv_fused_supported(int M, int K, int src, int epi);
+void launch_gemv_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s);
 // MFMA tile GEMM (gemm_i8_mfma.hip); any M.
 void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s);
 // 256x256-tile MFMA GEMM for large M, N (gemm_i8_mfma256.hip).

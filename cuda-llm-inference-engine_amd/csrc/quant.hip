@@ -16,11 +16,6 @@
 namespace ie {
 namespace {
 
-__device__ __forceinline__ uint32_t q8(float x, float inv) {
-    float r = fminf(fmaxf(rintf(x * inv), -128.0f), 127.0f);
-    return (uint32_t)((int32_t)r) & 0xffu;
-}
-
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     int cols, const float* __restrict__ in, int32_t* __restrict__ out,
     float* __restrict__ scales) {
@@ -39,16 +34,13 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     __syncthreads();
     m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
 
-    const float scale = (m > 0.0f) ? m / 127.0f : 1.0f;
+    const float scale = quant_scale(m);
     const float inv = 1.0f / scale;
     if (threadIdx.x == 0) scales[row] = scale;
 
     int32_t* o = out + (size_t)row * n4;
     for (int i = threadIdx.x; i < n4; i += 256) {
-        const float4 v = x[i];
-        const uint32_t w = q8(v.x, inv) | (q8(v.y, inv) << 8) | (q8(v.z, inv) << 16) |
-                           (q8(v.w, inv) << 24);
-        o[i] = (int32_t)w;
+        o[i] = quant_word(x[i], inv);
     }
 }
 

@@ -2,7 +2,7 @@
 // LayerNorm, token+position embedding, fp32 vocabulary projection and a
 // device-side argmax.  They run once or twice per layer on [M, d] rows, so they
 // are written for low latency, not as roofline kernels.
-#include <cfloat>
+#include <climits>
 
 #include "device_util.h"
 #include "ie_internal.h"
@@ -10,37 +10,40 @@
 namespace ie {
 namespace {
 
-// kernels/layernorm/15_layernorm_residual.cu:59-103: mean = E[x],
-// var = E[x^2] - mean^2, out = gamma * (x - mean) * rsqrt(var + eps) + beta.
-// One workgroup per row; in place (out == x) is allowed because every element
-// is read and written by the same thread.
-__global__ __launch_bounds__(256) void layernorm_kernel(int cols, const float* x,
+// kernels/layernorm/15_layernorm_residual.cu:59-103 (ln_accum / ln_finish /
+// ln_apply).  One wave per row, four rows per workgroup, no barrier.  In
+// place (out == x) is allowed: every element is read and written by the same
+// lane.  VEC: cols % 4 == 0 and 16-byte aligned rows (the GEMV prologue's
+// order); otherwise lanes take single elements l, l + 64, ...
+template <bool VEC>
+__global__ __launch_bounds__(256) void layernorm_kernel(int rows, int cols, const float* x,
                                                         const float* __restrict__ gamma,
                                                         const float* __restrict__ beta,
                                                         float* out, float eps) {
-    const float* xr = x + (size_t)blockIdx.x * cols;
-    float* orow = out + (size_t)blockIdx.x * cols;
-    float s = 0.0f, s2 = 0.0f;
-    for (int c = threadIdx.x; c < cols; c += 256) {
-        const float v = xr[c];
-        s += v;
-        s2 = fmaf(v, v, s2);
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const float* xr = x + (size_t)row * cols;
+    float* orow = out + (size_t)row * cols;
+    float s = 0.0f, s2 = 0.0f, mean, rs;
+    if constexpr (VEC) {
+        const int n4 = cols >> 2;
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        for (int j = lane; j < n4; j += 64) ln_accum(x4[j], s, s2);
+        ln_finish(s, s2, cols, eps, mean, rs);
+        const float4* g4 = reinterpret_cast<const float4*>(gamma);
+        const float4* b4 = reinterpret_cast<const float4*>(beta);
+        float4* o4 = reinterpret_cast<float4*>(orow);
+        for (int j = lane; j < n4; j += 64) o4[j] = ln_apply(x4[j], g4[j], b4[j], mean, rs);
+    } else {
+        for (int c = lane; c < cols; c += 64) {
+            const float v = xr[c];
+            s += v;
+            s2 = fmaf(v, v, s2);
+        }
+        ln_finish(s, s2, cols, eps, mean, rs);
+        for (int c = lane; c < cols; c += 64) orow[c] = fmaf(gamma[c] * (xr[c] - mean), rs, beta[c]);
     }
-    s = wave_sum(s);
-    s2 = wave_sum(s2);
-    __shared__ float red[2][4];
-    if ((threadIdx.x & 63) == 0) {
-        red[0][threadIdx.x >> 6] = s;
-        red[1][threadIdx.x >> 6] = s2;
-    }
-    __syncthreads();
-    s = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
-    s2 = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-    const float mean = s / cols;
-    const float var = s2 / cols - mean * mean;
-    const float inv = rsqrtf(var + eps);
-    for (int c = threadIdx.x; c < cols; c += 256)
-        orow[c] = gamma[c] * (xr[c] - mean) * inv + beta[c];
 }
 
 // kernels/layernorm/15_embed.cu:4-21.
@@ -109,42 +112,62 @@ __global__ __launch_bounds__(256) void vocab_proj_kernel(int rows, const float* 
     if (ok && li < rows && li < RT) logits[(size_t)li * V + j] = mine;
 }
 
-// src/sampler.cu:10-14 on the device: first index of the maximum.
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                     int* __restrict__ out) {
+// src/sampler.cu:10-14 on the device: first index of the maximum (ties go to
+// the lower index, as std::max_element).  One 1024-thread workgroup per row;
+// each thread issues 16 independent loads per round (a wave instruction reads
+// 256 contiguous bytes), so a 50257-wide row takes four memory round trips.
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxUnroll = 16;
+
+__device__ __forceinline__ void argmax_take(float& best, int& bi, float v, int i) {
+    if (v > best || (v == best && i < bi)) {
+        best = v;
+        bi = i;
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits,
+                                                                int n, int* __restrict__ out) {
     const float* x = logits + (size_t)blockIdx.x * n;
-    float best = -FLT_MAX;
-    int bi = n;  // sentinel larger than any index
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float v = x[i];
-        if (v > best || (bi == n && v == best)) {
-            best = v;
-            bi = i;
+    float best = -INFINITY;
+    int bi = INT_MAX;
+    for (int base = threadIdx.x; base < n; base += kArgmaxThreads * kArgmaxUnroll) {
+        float v[kArgmaxUnroll];
+#pragma unroll
+        for (int u = 0; u < kArgmaxUnroll; ++u) {
+            const int i = base + u * kArgmaxThreads;
+            v[u] = i < n ? x[i] : -INFINITY;
+        }
+        // A thread's indices increase, so a strict > keeps its first maximum;
+        // the first element it sees is always taken (an all -inf row still
+        // reports an index).
+#pragma unroll
+        for (int u = 0; u < kArgmaxUnroll; ++u) {
+            const int i = base + u * kArgmaxThreads;
+            if (i < n && (v[u] > best || bi == INT_MAX)) {
+                best = v[u];
+                bi = i;
+            }
         }
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ob = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (ob > best || (ob == best && oi < bi)) {
-            best = ob;
-            bi = oi;
-        }
-    }
-    __shared__ float sb[4];
-    __shared__ int si[4];
+    for (int off = 32; off > 0; off >>= 1)
+        argmax_take(best, bi, __shfl_xor(best, off, 64), __shfl_xor(bi, off, 64));
+    constexpr int W = kArgmaxThreads / 64;
+    __shared__ float sb[W];
+    __shared__ int si[W];
     if ((threadIdx.x & 63) == 0) {
         sb[threadIdx.x >> 6] = best;
         si[threadIdx.x >> 6] = bi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
-            if (sb[w] > best || (sb[w] == best && si[w] < bi)) {
-                best = sb[w];
-                bi = si[w];
-            }
-        out[blockIdx.x] = bi < n ? bi : 0;
+    if (threadIdx.x < 64) {
+        best = threadIdx.x < W ? sb[threadIdx.x] : -INFINITY;
+        bi = threadIdx.x < W ? si[threadIdx.x] : INT_MAX;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            argmax_take(best, bi, __shfl_xor(best, off, 64), __shfl_xor(bi, off, 64));
+        if (threadIdx.x == 0) out[blockIdx.x] = bi < n ? bi : 0;
     }
 }
 
@@ -153,7 +176,13 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ l
 void launch_layernorm(int rows, int cols, const float* x, const float* g, const float* b,
                       float* out, float eps, hipStream_t s) {
     if (rows == 0) return;
-    layernorm_kernel<<<rows, 256, 0, s>>>(cols, x, g, b, out, eps);
+    const bool vec = cols % 4 == 0 && (((uintptr_t)x | (uintptr_t)g | (uintptr_t)b |
+                                        (uintptr_t)out) % 16) == 0;
+    const unsigned blocks = (unsigned)((rows + 3) / 4);
+    if (vec)
+        layernorm_kernel<true><<<blocks, 256, 0, s>>>(rows, cols, x, g, b, out, eps);
+    else
+        layernorm_kernel<false><<<blocks, 256, 0, s>>>(rows, cols, x, g, b, out, eps);
 }
 
 void launch_embedding(const int* ids, int seq_len, int start_pos, int d, const float* wte,
@@ -184,7 +213,7 @@ void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits
 
 void launch_argmax(int rows, const float* logits, int n, int* out, hipStream_t s) {
     if (rows == 0) return;
-    argmax_kernel<<<rows, 256, 0, s>>>(logits, n, out);
+    argmax_kernel<<<rows, kArgmaxThreads, 0, s>>>(logits, n, out);
 }
 
 }  // namespace ie

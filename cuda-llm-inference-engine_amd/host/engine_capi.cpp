@@ -61,7 +61,7 @@ extern "C" {
 
 int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n_heads, int d_model,
                      int d_ff, int vocab_size, int max_seq_len, unsigned long long seed, int max_batch,
-                     int kv_dtype, int int8_lm_head, int use_graph) {
+                     int kv_dtype, int int8_lm_head, int use_graph, int fuse) {
     if (!out) return ie::fail(IE_ERR_INVALID, "ie_engine_create: out is null");
     *out = nullptr;
     GPT2EngineOptions opt;
@@ -69,6 +69,7 @@ int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n
     opt.kv_dtype = kv_dtype;
     opt.int8_lm_head = int8_lm_head != 0;
     opt.use_graph = use_graph != 0;
+    opt.fuse = fuse != 0;
     return guarded("ie_engine_create", [&] {
         GPT2Engine* e = model_dir ? new GPT2Engine(std::string(model_dir), opt)
                                   : new GPT2Engine(make_cfg(n_layers, n_heads, d_model, d_ff, vocab_size,

@@ -254,6 +254,8 @@ struct GPT2Engine::Impl {
     int *block_table = nullptr, *positions = nullptr, *ctx_lens = nullptr, *tokens = nullptr;
     float* ws = nullptr;
     size_t ws_bytes = 0;
+    int attn_splits = 1, attn_bps = 1;
+    bool fused = false;  // fused step kernels apply to this model
 
     int pos = 0;  // host mirror: tokens in every active sequence
     int* host_tokens = nullptr;  // pinned [max_batch]
@@ -341,6 +343,16 @@ struct GPT2Engine::Impl {
         const int S = ie_decode_num_splits(cfg.max_seq_len, kBlock, 0);
         ws_bytes = ie_decode_attn_workspace_bytes(B, cfg.n_heads, cfg.d_head, S);
         ws = dev<float>(ws_bytes / sizeof(float));
+        // Split plan of ie_decode_attn for max_context_len = max_seq_len.
+        attn_splits = S;
+        attn_bps = (nbps + S - 1) / S;
+        fused = opt.fuse && (cfg.d_head == 64 || cfg.d_head == 128);
+        for (int m = 1; m <= B && fused; ++m)
+            fused = ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, ie::kEpiQKV) &&
+                    ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, IE_EPI_BIAS_GELU) &&
+                    ie::gemv_fused_supported(m, d, ie::kSrcQuant, IE_EPI_BIAS_RESIDUAL) &&
+                    ie::gemv_fused_supported(m, ff, ie::kSrcQuant, IE_EPI_BIAS_RESIDUAL) &&
+                    ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, IE_EPI_PLAIN);
         HIPC(hipHostMalloc(&host_tokens, sizeof(int) * B));
         reset();
     }
@@ -363,9 +375,70 @@ struct GPT2Engine::Impl {
     void* layer_k(int l) { return kc + layer_elems * (opt.kv_dtype == IE_KV_BF16 ? 2 : 4) * l; }
     void* layer_v(int l) { return vc + layer_elems * (opt.kv_dtype == IE_KV_BF16 ? 2 : 4) * l; }
 
+    // GEMV with its activation operand built from fp32 rows in the kernel.
+    void fused_gemv(int B, const QuantWeight& w, int src, const float* xin, const float* g,
+                    const float* b, int epi, const float* bias, const float* res, float* out,
+                    const ie::GemvFusion* qkv_io = nullptr) {
+        ie::GemmArgs a{};
+        a.M = B; a.N = w.N; a.K = w.K;
+        a.BT = w.packed; a.sB = w.scale;
+        a.bias = bias; a.residual = res; a.C = out; a.epi = epi;
+        ie::GemvFusion f = qkv_io ? *qkv_io : ie::GemvFusion{};
+        f.src = src; f.x = xin; f.gamma = g; f.beta = b; f.eps = 1e-5f;
+        ie::launch_gemv_fused(a, f, stream);
+        IEC(ie::check_launch("fused gemv"));
+    }
+
+    // The decode step with LayerNorm / quantizer prologues and the QKV-append
+    // epilogue: 6 launches per layer.  Same
+    // operations and order as enqueue_step_unfused.
+    void enqueue_step_fused(int B) {
+        const int d = cfg.d_model, H = cfg.n_heads;
+        hipStream_t s = stream;
+        IEC(ie_embedding_batch(B, tokens, positions, d, wte, wpe, x, (ie_stream_t)s));
+        for (int l = 0; l < cfg.n_layers; ++l) {
+            const Layer& L = layers[l];
+            ie::GemvFusion io{};
+            io.q = q; io.kc = layer_k(l); io.vc = layer_v(l); io.kv_dtype = opt.kv_dtype;
+            io.positions = positions; io.table = block_table; io.nbps = nbps; io.block_size = kBlock;
+            io.ctx_lens = ctx_lens;
+            fused_gemv(B, L.qkv, ie::kSrcLnQuant, x, L.ln1_g, L.ln1_b, ie::kEpiQKV, L.qkv_b, nullptr,
+                       nullptr, &io);
+            ie::DecodeArgs a{};
+            a.B = B; a.H_q = H; a.H_kv = H; a.d = cfg.d_head;
+            a.Q = q; a.k_cache = layer_k(l); a.v_cache = layer_v(l); a.kv_dtype = opt.kv_dtype;
+            a.block_table = block_table; a.context_lens = ctx_lens;
+            a.block_size = kBlock; a.num_blocks_per_seq = nbps;
+            a.num_splits = attn_splits; a.blocks_per_split = attn_bps;
+            a.O = attn; a.workspace = ws;
+            ie::launch_decode_attn(a, s);
+            IEC(ie::check_launch("decode_attn"));
+            fused_gemv(B, L.out, ie::kSrcQuant, attn, nullptr, nullptr, IE_EPI_BIAS_RESIDUAL, L.out_b, x, x);
+            fused_gemv(B, L.up, ie::kSrcLnQuant, x, L.ln2_g, L.ln2_b, IE_EPI_BIAS_GELU, L.up_b, nullptr, h);
+            fused_gemv(B, L.down, ie::kSrcQuant, h, nullptr, nullptr, IE_EPI_BIAS_RESIDUAL, L.down_b, x, x);
+        }
+        if (opt.int8_lm_head) {
+            fused_gemv(B, head, ie::kSrcLnQuant, x, lnf_g, lnf_b, IE_EPI_PLAIN, nullptr, nullptr, logits);
+        } else {
+            IEC(ie_layernorm(B, d, x, lnf_g, lnf_b, xn, 1e-5f, (ie_stream_t)s));
+            IEC(ie_vocab_proj(B, xn, wte, logits, d, cfg.vocab_size, (ie_stream_t)s));
+        }
+        IEC(ie_argmax(B, logits, cfg.vocab_size, tokens, (ie_stream_t)s));
+        ie::launch_advance(B, positions, s);
+        IEC(ie::check_launch("advance"));
+    }
+
+    void enqueue_step(int B) {
+        if (fused)
+            enqueue_step_fused(B);
+        else
+            enqueue_step_unfused(B);
+    }
+
     // One decode step for B sequences: reads tokens/positions on the device,
     // leaves logits, writes the argmax into tokens and advances positions.
-    void enqueue_step(int B) {
+    // Every operation goes through the public C ABI.
+    void enqueue_step_unfused(int B) {
         const int d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size, H = cfg.n_heads;
         hipStream_t s = stream;
         ie_stream_t st = (ie_stream_t)s;

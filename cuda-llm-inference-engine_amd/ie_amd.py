@@ -47,7 +47,7 @@ SIGNATURES = {
 # include/ie_engine.h
 ENGINE_SIGNATURES = {
     "ie_engine_create": (_I, [ctypes.POINTER(_P), ctypes.c_char_p, _I, _I, _I, _I, _I, _I,
-                              ctypes.c_ulonglong, _I, _I, _I, _I]),
+                              ctypes.c_ulonglong, _I, _I, _I, _I, _I]),
     "ie_engine_destroy": (_I, [_P]),
     "ie_engine_write_random_model": (_I, [ctypes.c_char_p, _I, _I, _I, _I, _I, _I, ctypes.c_ulonglong]),
     "ie_engine_reset": (_I, [_P]),
@@ -256,14 +256,14 @@ class Engine:
     random model of the given shape (GPT-2 Small by default)."""
 
     def __init__(self, model_dir=None, seed=0, max_batch=1, kv_dtype=KV_F32, int8_lm_head=False,
-                 use_graph=True, **cfg):
+                 use_graph=True, fuse=True, **cfg):
         import numpy as np  # noqa: F401
 
         c = dict(GPT2_SMALL, **cfg)
         h = ctypes.c_void_p()
         check("ie_engine_create", ctypes.byref(h), None if model_dir is None else str(model_dir).encode(),
               c["n_layers"], c["n_heads"], c["d_model"], c["d_ff"], c["vocab_size"], c["max_seq_len"], seed,
-              max_batch, kv_dtype, int(int8_lm_head), int(use_graph))
+              max_batch, kv_dtype, int(int8_lm_head), int(use_graph), int(fuse))
         self.h = h
         v = (ctypes.c_int * 7)()
         check("ie_engine_config", h, ctypes.cast(v, ctypes.c_void_p))

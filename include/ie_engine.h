@@ -26,11 +26,12 @@ typedef struct {
 } ie_metrics;
 
 /* model_dir != NULL loads the reference on-disk format and ignores the
- * shape arguments; model_dir == NULL builds a random model of that shape. */
+ * shape arguments; model_dir == NULL builds a random model of that shape.
+ * fuse selects the fused decode step (GPT2EngineOptions::fuse). */
 int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n_heads,
                      int d_model, int d_ff, int vocab_size, int max_seq_len,
                      unsigned long long seed, int max_batch, int kv_dtype,
-                     int int8_lm_head, int use_graph);
+                     int int8_lm_head, int use_graph, int fuse);
 int ie_engine_destroy(ie_engine* e);
 int ie_engine_write_random_model(const char* dir, int n_layers, int n_heads, int d_model,
                                  int d_ff, int vocab_size, int max_seq_len,

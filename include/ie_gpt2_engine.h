@@ -68,6 +68,10 @@ struct GPT2EngineOptions {
     int kv_dtype = IE_KV_F32;   /* IE_KV_F32 (reference) or IE_KV_BF16 */
     bool int8_lm_head = false;  /* reference: fp32 head over tied wte */
     bool use_graph = true;      /* replay one captured decode step per token */
+    /* Fused decode step: LayerNorm and the activation quantizer run inside
+     * the GEMVs and QKV appends to the KV cache in its epilogue (GPT-2
+     * widths d = 768, ff = 3072; other shapes use the unfused step). */
+    bool fuse = true;
 };
 
 class GPT2Engine {

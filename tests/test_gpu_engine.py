@@ -7,9 +7,10 @@ invariance (both bit-exact), and the bf16-KV / INT8-head variants.
 
 Parity bar for the engine against the oracle: the oracle's LayerNorm runs in
 fp64 and the device's in fp32, so an activation can land on the other side of
-an int8 rounding boundary; logits are held to max|diff| <= 2e-3 * max|logits|
-and the greedy token must agree whenever the oracle's top-2 gap exceeds 1e-2 of
-the logit scale.
+an int8 rounding boundary.  For the 128-wide model logits are held to
+max|diff| <= 2e-3 * max|logits| and the greedy token must agree whenever the
+oracle's top-2 gap exceeds 1e-2 of the logit scale; for the 768-wide model see
+check_steps.  The fused step is held to bit-identity with the unfused one.
 """
 import numpy as np
 import pytest
@@ -17,12 +18,22 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 TINY = dict(n_layers=2, n_heads=2, d_model=128, d_ff=512, vocab_size=1000, max_seq_len=64)
+# GPT-2 widths (the fused step's kernels), few layers, small vocabulary; 256
+# positions give 4 attention splits of 64 tokens.
+MID = dict(n_layers=2, n_heads=12, d_model=768, d_ff=3072, vocab_size=1000, max_seq_len=256)
 
 
 @pytest.fixture(scope="module")
 def tiny_dir(tmp_path_factory, ie):
     d = tmp_path_factory.mktemp("gpt2_tiny")
     ie.write_random_model(d, seed=11, **TINY)
+    return d
+
+
+@pytest.fixture(scope="module")
+def mid_dir(tmp_path_factory, ie):
+    d = tmp_path_factory.mktemp("gpt2_mid")
+    ie.write_random_model(d, seed=12, **MID)
     return d
 
 
@@ -117,3 +128,82 @@ def test_gpt2_small_random_generates(ie):
     one, _ = eng.generate(prompt[:1], 8, ignore_eos=True)
     assert np.array_equal(one[0], a[0])
     assert m["tps"] > 0
+
+
+def check_steps(errs):
+    """Per-step max |diff| / max |logits| for the 768-wide model.  At this
+    width an activation now and then lies within fp32-vs-fp64 noise of an int8
+    rounding boundary and is quantized one step apart; the step's K/V then stay
+    in the cache, so the sequence's later logits move too.  Running the oracle
+    itself with 1e-7 relative noise on its LayerNorm outputs (3 sequences x 60
+    steps, this model) moves logits by up to 2.1e-2 of their scale, and the
+    device shows the same events.  Bar: every step within 3e-2, and steps
+    before the first such event within fp32 rounding (1e-5)."""
+    errs = np.asarray(errs)
+    assert errs.max() <= 3e-2, errs
+    first = int(np.argmax(errs > 1e-5)) if (errs > 1e-5).any() else len(errs)
+    assert (errs[:first] <= 1e-5).all()
+
+
+def check_vs_oracle(ie, model_dir, B, steps, seed, eng_kw, orc_kw):
+    from oracle.gpt2_step import OracleGPT2
+
+    rng = np.random.default_rng(seed)
+    toks = rng.integers(0, 1000, (steps, B)).astype(np.int32)
+    eng = ie.Engine(model_dir, max_batch=B, **eng_kw)
+    om = OracleGPT2(str(model_dir), batch=B, **orc_kw)
+    errs = []
+    for t in toks:
+        got, want = eng.step(t), om.step(t)
+        sc = np.abs(want).max()
+        errs.append([np.abs(got[b] - want[b]).max() / sc for b in range(B)])
+        # the greedy token agrees wherever a quantization flip cannot reorder it
+        for b in range(B):
+            top = np.sort(want[b])[-2:]
+            if top[1] - top[0] > 6e-2 * sc:
+                assert np.argmax(got[b]) == np.argmax(want[b])
+    eng.close()
+    for b in range(B):
+        check_steps([e[b] for e in errs])
+
+
+@pytest.mark.parametrize("B", [1, 3, 6])
+def test_gpt2_width_step_matches_oracle(ie, mid_dir, B):
+    """The (fused) step against the oracle; 70 steps cross the first 64-token
+    split boundary."""
+    check_vs_oracle(ie, mid_dir, B, 70, 20 + B, {}, {})
+
+
+def test_gpt2_width_bf16_kv_and_int8_head(ie, mid_dir):
+    check_vs_oracle(ie, mid_dir, 2, 20, 5, dict(kv_dtype=ie.KV_BF16), dict(kv_bf16=True))
+    check_vs_oracle(ie, mid_dir, 5, 20, 6, dict(int8_lm_head=True), dict(int8_lm_head=True))
+
+
+@pytest.mark.parametrize("B", [1, 3, 6])
+def test_fused_step_bit_identical_to_unfused_step(ie, mid_dir, B):
+    """The fused kernels (LayerNorm/quantizer prologues, QKV append epilogue)
+    against the step built from the public C ABI
+    operations: same arithmetic in the same order, so bit-identical logits,
+    including past the first 64-token split boundary."""
+    rng = np.random.default_rng(30 + B)
+    toks = rng.integers(0, 1000, (70, B)).astype(np.int32)
+    for kw in (dict(), dict(kv_dtype=ie.KV_BF16, int8_lm_head=True)):
+        a = run_steps(ie.Engine(mid_dir, max_batch=B, fuse=True, **kw), toks)
+        b = run_steps(ie.Engine(mid_dir, max_batch=B, fuse=False, **kw), toks)
+        for i, (x, y) in enumerate(zip(a, b)):
+            assert np.array_equal(x, y), (kw, i, np.abs(x - y).max())
+
+
+def test_fused_graph_replay_and_batch_invariance(ie, mid_dir):
+    rng = np.random.default_rng(7)
+    toks = rng.integers(0, 1000, (12, 5)).astype(np.int32)
+    a = run_steps(ie.Engine(mid_dir, max_batch=5, use_graph=True), toks)
+    b = run_steps(ie.Engine(mid_dir, max_batch=5, use_graph=False), toks)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    # rows of a batch-5 step equal the batch-1 runs bit for bit (the fixed and
+    # the MFMA GEMV stage activation rows identically)
+    for i in (0, 4):
+        one = run_steps(ie.Engine(mid_dir, max_batch=1), toks[:, i:i + 1])
+        for x, y in zip(a, one):
+            assert np.array_equal(x[i], y[0])
