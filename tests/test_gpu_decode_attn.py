@@ -145,6 +145,28 @@ def test_explicit_split_counts(ie, orc, splits):
     assert rel_err(got, want) < REL
 
 
+@pytest.mark.parametrize("kvdt", [0, 1])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_one_wave_and_four_wave_splits(ie, orc, G, d, kvdt):
+    """Splits of >= 256 tokens run on one wave each, shorter ones on four waves
+    that merge in LDS: both layouts for every head width, group size and KV
+    type (max_context_len 700: 1 and 2 splits are one-wave, 3 and 11 are
+    four-wave)."""
+    r = rng(1000 + 10 * G + d + kvdt)
+    B, H_kv = 2, 2
+    H_q = H_kv * G
+    lens = np.array([700, 300])
+    kc, vc, table, _, _ = make_paged_cache(r, B, H_kv, d, lens, 16)
+    Q = r.standard_normal((B, H_q, d)).astype(np.float32)
+    if kvdt:
+        kc, vc = bf16_bits(kc), bf16_bits(vc)
+    want = orc.decode_attn(Q, kc, vc, table, lens, 700, 16, H_kv, kv_dtype=kvdt)
+    for splits in (1, 2, 3, 11):
+        got = run_gpu(ie, Q, kc, vc, table, lens, 700, 16, H_kv, kv_dtype=kvdt, splits=splits)
+        assert rel_err(got, want) < REL, splits
+
+
 def test_edges(ie, orc):
     r = rng(8)
     B, H, d = 3, 4, 64
