@@ -132,8 +132,7 @@ __device__ __forceinline__ void consume_chunk(const Chunk<D, KV>& c, const float
             s[j] = c.valid[j] ? dot : -INFINITY;
         }
         float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        cm = fmaxf(cm, xor16(cm));
-        cm = fmaxf(cm, xor32(cm));
+        cm = max_xor32(max_xor16(cm));
         const float mn = fmaxf(m[g], cm);
         const float alpha = exp2f(m[g] - mn);
         float p[4], psum = 0.0f;
@@ -278,12 +277,10 @@ __global__ __launch_bounds__(64 * WPS) void decode_attn_split_kernel(
     // The four lane rows share the wave's running max: plain sums merge them.
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        l[g] += xor16(l[g]);
-        l[g] += xor32(l[g]);
+        l[g] = sum_xor32(sum_xor16(l[g]));
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
-            o[g][e] += xor16(o[g][e]);
-            o[g][e] += xor32(o[g][e]);
+            o[g][e] = sum_xor32(sum_xor16(o[g][e]));
         }
     }
     // The partial of this split; an empty split writes o = 0, m = -inf, l = 0.

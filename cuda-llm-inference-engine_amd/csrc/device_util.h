@@ -41,20 +41,59 @@ __device__ __forceinline__ int row16_sum(int v) {
     return v;
 }
 
-// Exchange between the four 16-lane rows of a wave (lane ^ 16, lane ^ 32).
-__device__ __forceinline__ float xor16(float v) { return __shfl_xor(v, 16, 64); }
-__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+// Combining the four 16-lane rows of a wave with gfx950's v_permlane16_swap /
+// v_permlane32_swap (plain VALU ops, no LDS round trip as ds_bpermute has):
+// with both registers holding v, lane l ends with {v[l & ~16], v[l | 16]}
+// (resp. 32), so op(lo, hi) is the same value in both lanes of a pair, in a
+// fixed order.  The instruction rewrites both of its registers; it is issued
+// from inline assembly because the compiler's builtin (ROCm 7.2) drops the
+// second result when both operands hold the same value.  The leading s_nop
+// covers the VALU-write-then-permlane-read hazard, as the compiler does for
+// the builtin.
+__device__ __forceinline__ void pair16(float v, float& lo, float& hi) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    __asm__ volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    lo = __builtin_bit_cast(float, a);
+    hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ void pair32(float v, float& lo, float& hi) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    __asm__ volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    lo = __builtin_bit_cast(float, a);
+    hi = __builtin_bit_cast(float, b);
+}
+// v + v[l ^ 16] and v + v[l ^ 32] (rows paired), and the max forms.
+__device__ __forceinline__ float sum_xor16(float v) {
+    float a, b;
+    pair16(v, a, b);
+    return a + b;
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    float a, b;
+    pair32(v, a, b);
+    return a + b;
+}
+__device__ __forceinline__ float max_xor16(float v) {
+    float a, b;
+    pair16(v, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    float a, b;
+    pair32(v, a, b);
+    return fmaxf(a, b);
+}
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+// Whole-wave reductions: DPP within each row, then the row pairs.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_row_ror<8>(v));
+    v = fmaxf(v, dpp_row_ror<4>(v));
+    v = fmaxf(v, dpp_row_ror<2>(v));
+    v = fmaxf(v, dpp_row_ror<1>(v));
     return v;
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return max_xor32(max_xor16(row16_max(v))); }
+__device__ __forceinline__ float wave_sum(float v) { return sum_xor32(sum_xor16(row16_sum(v))); }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __builtin_bit_cast(float, (uint32_t)h << 16);
