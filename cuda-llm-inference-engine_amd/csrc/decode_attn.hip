@@ -116,6 +116,22 @@ __device__ __forceinline__ void load_chunk(Chunk<D, KV>& c, int c0, int grp, int
     }
 }
 
+// Block size 16: all 16 tokens of the chunk (c0 a multiple of 16) lie in
+// physical block `phys`, the same for every lane.
+template <int D, typename KV>
+__device__ __forceinline__ void load_chunk16(Chunk<D, KV>& c, int c0, int grp, int tok1, int phys,
+                                             size_t tok_stride, const KV* kbase, const KV* vbase) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int pos = c0 + 4 * j + grp;
+        c.valid[j] = pos < tok1;
+        const int pc = min(pos, tok1 - 1);
+        const size_t row = (size_t)phys * 16 + (pc & 15);
+        load_raw(kbase + row * tok_stride, c.k[j]);
+        load_raw(vbase + row * tok_stride, c.v[j]);
+    }
+}
+
 template <int D, int G, typename KV>
 __device__ __forceinline__ void consume_chunk(const Chunk<D, KV>& c, const float (&q)[G][D / 16],
                                               float (&m)[G], float (&l)[G], float (&o)[G][D / 16]) {
@@ -213,7 +229,8 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ w, int S,
 
 // WPS waves per split: 4 for short splits (the waves take the split's chunks
 // round-robin and merge in LDS), 1 for long ones (no LDS merge, no barrier).
-template <int D, int G, typename KV, int WPS>
+// BS16: block_size == 16 (the engine's and the reference's), see below.
+template <int D, int G, typename KV, int WPS, bool BS16>
 __global__ __launch_bounds__(64 * WPS) void decode_attn_split_kernel(
     const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
     const int* __restrict__ block_table, const int* __restrict__ context_lens, int H_q,
@@ -221,7 +238,8 @@ __global__ __launch_bounds__(64 * WPS) void decode_attn_split_kernel(
     float* __restrict__ ws) {
     constexpr int EPL = D / 16;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = WPS == 1 ? 0 : threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = WPS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane >> 4, li = lane & 15;
     constexpr int STEP = 16 * WPS;  // tokens per round of the split's waves
 
@@ -240,10 +258,31 @@ __global__ __launch_bounds__(64 * WPS) void decode_attn_split_kernel(
     const KV* vbase = vcache + (size_t)kvh * D + li * EPL;
 
     // Each wave walks its chunks of 16 tokens, keeping the next chunk's loads
-    // in flight while it computes the current one.
+    // in flight while it computes the current one.  With block size 16 a
+    // chunk is one block, so its physical block id is wave-uniform: it comes
+    // from a scalar load issued one chunk ahead (phys), which does not wait
+    // behind the in-flight KV loads as a vector load would (they retire in
+    // issue order), so the next KV loads go out as soon as a chunk is done.
     Chunk<D, KV> ca, cb;
     int c0 = tok0 + wave * 16;
-    if (c0 < tok1) load_chunk(ca, c0, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+    auto phys = [&](int cs) { return bt[min(cs, tok1 - 1) >> 4]; };
+    int pn = 0;
+    if (c0 < tok1) {
+        if constexpr (BS16) {
+            load_chunk16(ca, c0, grp, tok1, phys(c0), tok_stride, kbase, vbase);
+            pn = phys(c0 + STEP);
+        } else {
+            load_chunk(ca, c0, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+        }
+    }
+    auto next = [&](Chunk<D, KV>& c, int cs) {
+        if constexpr (BS16) {
+            load_chunk16(c, cs, grp, tok1, pn, tok_stride, kbase, vbase);
+            pn = phys(cs + STEP);
+        } else {
+            load_chunk(c, cs, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+        }
+    };
 
     float q[G][EPL];
 #pragma unroll
@@ -265,11 +304,11 @@ __global__ __launch_bounds__(64 * WPS) void decode_attn_split_kernel(
     // Ping-pong: the loads for chunk c0+STEP are always issued (clamped past
     // the end) before chunk c0 is consumed.
     while (c0 < tok1) {
-        load_chunk(cb, c0 + STEP, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+        next(cb, c0 + STEP);
         consume_chunk<D, G, KV>(ca, q, m, l, o);
         c0 += STEP;
         if (c0 >= tok1) break;
-        load_chunk(ca, c0 + STEP, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+        next(ca, c0 + STEP);
         consume_chunk<D, G, KV>(cb, q, m, l, o);
         c0 += STEP;
     }
@@ -359,7 +398,14 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
     const float qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
     const dim3 grid(a.num_splits, a.H_kv, a.B);
     const bool wave = (long long)a.blocks_per_split * a.block_size >= kWaveSplitTokens;
-    auto* k = wave ? decode_attn_split_kernel<D, G, KV, 1> : decode_attn_split_kernel<D, G, KV, 4>;
+    // Scalar block ids measured 12% faster for bf16 KV at ctx 8192 and 1%
+    // slower for fp32 one-wave splits (where the per-lane table loads already
+    // sit behind the chunk's own KV loads); fp32 long splits keep those.
+    const bool bs16 = a.block_size == 16 && !(wave && sizeof(KV) == 4);
+    auto* k = wave ? (bs16 ? decode_attn_split_kernel<D, G, KV, 1, true>
+                           : decode_attn_split_kernel<D, G, KV, 1, false>)
+                   : (bs16 ? decode_attn_split_kernel<D, G, KV, 4, true>
+                           : decode_attn_split_kernel<D, G, KV, 4, false>);
     k<<<grid, wave ? 64 : 256, 0, s>>>(
         a.Q, static_cast<const KV*>(a.k_cache), static_cast<const KV*>(a.v_cache),
         a.block_table, a.context_lens, a.H_q, a.H_kv, a.block_size, a.num_blocks_per_seq,
