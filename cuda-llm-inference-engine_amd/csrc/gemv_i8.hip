@@ -152,7 +152,11 @@ __device__ __forceinline__ void dot_chunk(int32_t (&acc)[MT], const i32x4 wv, co
 //
 // With SRC != kSrcInt8 wave w builds activation row w itself (stage_row) while
 // the first weight loads are in flight, and the row scales come from LDS.
-template <int MT, int EPI, int K16, int SRC = kSrcInt8>
+//
+// NT: weight loads are non-temporal (streamed past the caches).  Used for
+// weight matrices too large to stay cache-resident between calls; measured
+// 10% faster at K = 8192, N = 28672.
+template <int MT, int EPI, int K16, int SRC = kSrcInt8, bool NT = false>
 __global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
     int M, int N, const int32_t* __restrict__ A, const int32_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
@@ -176,7 +180,12 @@ __global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
             const int n = r0 + g * 4 + (lane >> 4);
             const i32x4* w = w4 + (size_t)min(n, N - 1) * K16 + li;
 #pragma unroll
-            for (int t = 0; t < CPL; ++t) wv[g][t] = w[16 * t];
+            for (int t = 0; t < CPL; ++t) {
+                if constexpr (NT)
+                    wv[g][t] = __builtin_nontemporal_load(w + 16 * t);
+                else
+                    wv[g][t] = w[16 * t];
+            }
         }
     };
     int r0 = wave_global * (4 * G);
@@ -265,74 +274,120 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
 }
 
 // 5 <= M <= 16: v_mfma_i32_16x16x64_i8 with the activations (M padded to 16
-// rows, staged in LDS once per workgroup) as the A operand and 16 weight rows
-// per wave as the B operand.  Lane l feeds weight row n0 + l % 16, K-bytes
-// 16 * (l / 16) .. +16 of each 64-byte K step, so one 16-byte load per lane per
-// MFMA streams 1 KiB of weights; dot4 would need 4 instructions per weight
+// rows) as the A operand and 16 weight rows as the B operand.  A workgroup
+// owns 16 output features and its four waves split K four ways (so even
+// N = 768 spreads over 48 workgroups), each adding its int32 tile into LDS at
+// the end (exact).  Lane l feeds weight row n0 + l % 16, K-bytes
+// 16 * (l / 16) .. +16 of each 64-byte K step, so one 16-byte load per lane
+// per MFMA streams 1 KiB of weights; dot4 would need 4 instructions per weight
 // byte at M = 16, which caps it below HBM speed.  Accumulator v of lane l is
-// C[4 * (l / 16) + v][n0 + l % 16].
-// With SRC != kSrcInt8 wave w builds activation rows w, w + 4, ... itself.
-template <int EPI, int K64, int SRC = kSrcInt8>
+// C[4 * (l / 16) + v][n0 + l % 16].  For K <= 4096 the activation block is
+// staged in LDS (or built there by the fused prologue); beyond that each lane
+// reads its A fragment straight from global memory (the block is L2-resident).
+// Weight loads run U steps ahead of the MFMAs.
+template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false>
 __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
     int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
     const float* residual, void* C, GemvFusion f) {
     constexpr int K = K64 * 64;
-    constexpr int U = K64 % 8 == 0 ? 8 : (K64 % 4 == 0 ? 4 : 2);  // loads in flight per lane
-    __shared__ i32x4 a_lds[16 * K / 16];
+    static_assert(K64 % 4 == 0, "four waves split K");
+    constexpr int KW = K64 / 4;                // K steps per wave
+    constexpr bool A_LDS = K <= 4096;
+    static_assert(A_LDS || SRC == kSrcInt8, "fused prologues stage A in LDS");
+    // weight loads in flight per lane: the largest divisor of KW up to 8
+    constexpr int U = KW <= 8 ? KW : KW % 8 == 0 ? 8 : KW % 6 == 0 ? 6 : KW % 4 == 0 ? 4 : 2;
+    static_assert(KW % U == 0, "whole batches");
+    __shared__ i32x4 a_lds[A_LDS ? 16 * K / 16 : 1];
     __shared__ float s_sa[16];
-    if constexpr (SRC == kSrcInt8) {
-        for (int i = threadIdx.x; i < 16 * (K / 16); i += 256) {
-            const int m = i / (K / 16);
-            const int mm = m < M ? m : M - 1;
-            a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)mm * K)[i - m * (K / 16)];
-        }
-    } else {
-        for (int m = threadIdx.x >> 6; m < 16; m += 4) {
-            int32_t* dst = reinterpret_cast<int32_t*>(a_lds + m * (K / 16));
-            if (m < M)
-                stage_row<K, SRC>(f.x + (size_t)m * K, f, dst, &s_sa[m], threadIdx.x & 63);
-            else
-                zero_row<K>(dst, &s_sa[m], threadIdx.x & 63);
-        }
-    }
-    __syncthreads();
-    const float* sa_src = SRC == kSrcInt8 ? sA : s_sa;
-    const int lane = threadIdx.x & 63;
+    __shared__ i32x4 red[3][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, kq = lane >> 4;
-    const int wave_global = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int waves = gridDim.x * 4;
-    for (int n0 = wave_global * 16; n0 < N; n0 += waves * 16) {
-        const int8_t* w = BT + (size_t)min(n0 + col, N - 1) * K + kq * 16;
-        const i32x4* a = a_lds + col * (K / 16) + kq;
-        // Two accumulators alternate so consecutive MFMAs do not wait on each
-        // other; their integer sum is exact.
-        i32x4 acc = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
-#pragma unroll 1
-        for (int k0 = 0; k0 < K64; k0 += U) {
-            i32x4 wv[U];
+    const int n0 = blockIdx.x * 16;
+    const int kb = wave * KW;  // first K step of this wave
+
+    auto ldw = [&](const int8_t* p) {
+        if constexpr (NT)
+            return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+        else
+            return *reinterpret_cast<const i32x4*>(p);
+    };
+    const int8_t* w = BT + (size_t)min(n0 + col, N - 1) * K + kq * 16;
+    const int8_t* arow = A + (size_t)min(col, M - 1) * K + kq * 16;  // global A (K > 4096)
+    i32x4 wv[U], ag[A_LDS ? 1 : U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) wv[u] = *reinterpret_cast<const i32x4*>(w + (k0 + u) * 64);
-#pragma unroll
-            for (int u = 0; u < U; u += 2) {
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[(k0 + u) * 4], wv[u], acc, 0, 0, 0);
-                if (u + 1 < U)
-                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[(k0 + u + 1) * 4], wv[u + 1], acc1, 0, 0, 0);
+    for (int u = 0; u < U; ++u) {
+        wv[u] = ldw(w + (size_t)(kb + u) * 64);
+        if constexpr (!A_LDS) ag[u] = *reinterpret_cast<const i32x4*>(arow + (size_t)(kb + u) * 64);
+    }
+
+    if constexpr (A_LDS) {
+        if constexpr (SRC == kSrcInt8) {
+            for (int i = threadIdx.x; i < 16 * (K / 16); i += 256) {
+                const int m = i / (K / 16);
+                const int mm = m < M ? m : M - 1;
+                a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)mm * K)[i - m * (K / 16)];
+            }
+        } else {
+            for (int m = wave; m < 16; m += 4) {
+                int32_t* dst = reinterpret_cast<int32_t*>(a_lds + m * (K / 16));
+                if (m < M)
+                    stage_row<K, SRC>(f.x + (size_t)m * K, f, dst, &s_sa[m], lane);
+                else
+                    zero_row<K>(dst, &s_sa[m], lane);
             }
         }
-        acc += acc1;
-        const int n = n0 + col;
-        if (n < N) {
-            float sb = 0.0f;
-            if constexpr (EPI != IE_EPI_I32) sb = sB[n];
+        __syncthreads();
+    }
+    const float* sa_src = SRC == kSrcInt8 ? sA : s_sa;
+
+    // Two accumulators alternate so consecutive MFMAs do not wait on each
+    // other; their integer sum is exact.
+    i32x4 acc = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+#pragma unroll 1
+    for (int k0 = 0; k0 < KW; k0 += U) {
+        i32x4 av[U], cur[U];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int m = 4 * kq + v;
-                if (m < M) {
-                    float sa = 0.0f;
-                    if constexpr (EPI != IE_EPI_I32) sa = sa_src[m];
-                    gemv_store<EPI>(C, m, n, N, acc[v], sa, sb, bias, residual, f);
-                }
+        for (int u = 0; u < U; ++u) {
+            if constexpr (A_LDS)
+                av[u] = a_lds[col * (K / 16) + (kb + k0 + u) * 4 + kq];
+            else
+                av[u] = ag[u];
+            cur[u] = wv[u];
+        }
+        // next batch's weights (and global A fragments) in flight during the MFMAs
+        if (k0 + U < KW) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                wv[u] = ldw(w + (size_t)(kb + k0 + U + u) * 64);
+                if constexpr (!A_LDS) ag[u] = *reinterpret_cast<const i32x4*>(arow + (size_t)(kb + k0 + U + u) * 64);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u += 2) {
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u], cur[u], acc, 0, 0, 0);
+            if (u + 1 < U)
+                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u + 1], cur[u + 1], acc1, 0, 0, 0);
+        }
+    }
+    acc += acc1;
+    if (wave > 0) red[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave > 0) return;
+    acc += red[0][lane];
+    acc += red[1][lane];
+    acc += red[2][lane];
+    const int n = n0 + col;
+    if (n < N) {
+        float sb = 0.0f;
+        if constexpr (EPI != IE_EPI_I32) sb = sB[n];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int m = 4 * kq + v;
+            if (m < M) {
+                float sa = 0.0f;
+                if constexpr (EPI != IE_EPI_I32) sa = sa_src[m];
+                gemv_store<EPI>(C, m, n, N, acc[v], sa, sb, bias, residual, f);
             }
         }
     }
@@ -362,22 +417,50 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
     store_epilogue<EPI>(C, idx, s, sa, sb, bias, residual, n);
 }
 
+// Compute units of the current device (256 on MI355X), looked up once.
+int num_cus() {
+    static const int n = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        return v;
+    }();
+    return n;
+}
+
+// Weight matrices at least this large are streamed with non-temporal loads
+// (a quarter of the 256 MiB MALL: larger ones do not stay resident anyway).
+constexpr size_t kStreamWeightBytes = 64ull << 20;
+
 template <int MT, int EPI, int K16, int SRC = kSrcInt8>
 void launch_fixed(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFusion{}) {
     constexpr int CPL = K16 / 16;
     constexpr int G = CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;
     const int rows_per_wg = 4 * 4 * G;
-    const unsigned blocks = (unsigned)min((a.N + rows_per_wg - 1) / rows_per_wg, 2048);
-    gemv_i8_fixed_kernel<MT, EPI, K16, SRC><<<blocks, 256, 0, s>>>(
-        a.M, a.N, a.A, a.BT, a.sA, a.sB, a.bias, a.residual, a.C, f);
+    const bool nt = (size_t)a.N * K16 * 16 >= kStreamWeightBytes;
+    // Streaming shapes: one workgroup per CU walking row groups (each wave
+    // keeps a whole group's loads in flight); measured faster than one
+    // workgroup per 16 rows, which re-stages the activations in every
+    // workgroup and leaves a partial last wave of workgroups.
+    const int cap = nt ? num_cus() : 2048;
+    const unsigned blocks = (unsigned)min((a.N + rows_per_wg - 1) / rows_per_wg, cap);
+    if (nt)
+        gemv_i8_fixed_kernel<MT, EPI, K16, SRC, true><<<blocks, 256, 0, s>>>(
+            a.M, a.N, a.A, a.BT, a.sA, a.sB, a.bias, a.residual, a.C, f);
+    else
+        gemv_i8_fixed_kernel<MT, EPI, K16, SRC, false><<<blocks, 256, 0, s>>>(
+            a.M, a.N, a.A, a.BT, a.sA, a.sB, a.bias, a.residual, a.C, f);
 }
 
 template <int EPI, int K64, int SRC = kSrcInt8>
 void launch_mfma16(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFusion{}) {
-    const unsigned blocks = (unsigned)min((a.N + 63) / 64, 2048);
-    gemv_i8_mfma16_kernel<EPI, K64, SRC><<<blocks, 256, 0, s>>>(
-        a.M, a.N, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
-        a.sA, a.sB, a.bias, a.residual, a.C, f);
+    const unsigned blocks = (unsigned)((a.N + 15) / 16);
+    const bool nt = (size_t)a.N * K64 * 64 >= kStreamWeightBytes;
+    auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true> : gemv_i8_mfma16_kernel<EPI, K64, SRC, false>;
+    k<<<blocks, 256, 0, s>>>(a.M, a.N, reinterpret_cast<const int8_t*>(a.A),
+                             reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual,
+                             a.C, f);
 }
 
 template <int EPI, int K, int SRC>
@@ -394,12 +477,17 @@ void launch_mt(const GemmArgs& a, hipStream_t s) {
         if (a.K == 768) return launch_mfma16<EPI, 12>(a, s);
         if (a.K == 3072) return launch_mfma16<EPI, 48>(a, s);
     }
-    // Specialised K: the GPT-2 widths and the square 8192 shape, while the
-    // activation block fits the 48 KiB LDS budget.
+    // K = 8192: one row streams best with dot4; from two rows on, the dot4
+    // work per pass (no cross-pass prefetch at this K) outlasts the loads, so
+    // the MFMA kernel takes over.
+    if (a.K == 8192) {
+        if constexpr (MT == 1) return launch_fixed<1, EPI, 512>(a, s);
+        else return launch_mfma16<EPI, 128>(a, s);
+    }
+    // Specialised K: the GPT-2 widths.
     if constexpr (MT <= 4) {
         if (a.K == 768) return launch_fixed<MT, EPI, 48>(a, s);
         if (a.K == 3072) return launch_fixed<MT, EPI, 192>(a, s);
-        if (a.K == 8192 && MT == 1) return launch_fixed<MT, EPI, 512>(a, s);
     }
     const dim3 grid((a.N + kRowsPerWG - 1) / kRowsPerWG);
     gemv_i8_kernel<MT, EPI><<<grid, 256, 0, s>>>(a.M, a.N, a.K, a.A, a.BT, a.sA, a.sB, a.bias,
