@@ -167,6 +167,10 @@ void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s) {
         launch_gemm_i8_big(a, s);
         return;
     }
+    if (gemm_i8_stream_applies(a)) {
+        launch_gemm_i8_stream(a, s);
+        return;
+    }
     dispatch_epilogue<MfmaLaunch>(a.epi, a, s);
 }
 

@@ -1,0 +1,150 @@
+// gemm_i8_stream.hip — INT8 GEMM for mid-size problems (prefill-sized M, a
+// few hundred to a few thousand rows, GPT-2-sized N and K) on gfx950.
+//
+// Same result as the reference's K14 kernel (kernels/quantization/
+// 14_int8_gemm.cu:65-170): exact int32 K-sum, then the dequant epilogue.
+//
+// At these sizes a 256x256 (or 128x128) LDS-tiled workgroup leaves most of the
+// 256 CUs idle and spends its time in the per-step barrier, so here every wave
+// is independent: it owns a 32 x (32 * NB) block of C, held as NB
+// v_mfma_i32_32x32x32_i8 accumulators, and streams its A and B fragments
+// straight from global memory into registers one K-group ahead, with no LDS
+// and no barrier.  A K-group is 128 bytes of K = four MFMA K-steps:
+//   * lane l owns row l % 32 of the A block (and of each B block) and half
+//     h = l / 32 of the group's 128 bytes: one 64-byte contiguous run, read
+//     as four 16-byte loads, so the two lanes of a row cover its 128-byte
+//     line;
+//   * MFMA step s of the group takes chunk s of each lane's run: K-bytes
+//     128u + 16s (h = 0) and 128u + 64 + 16s (h = 1).  A and B use the same
+//     lane -> K map, so the four steps sum exactly the group's 128 bytes, in
+//     whatever order; the int32 result is the K-sum bit for bit.
+// Accumulator v of lane l is C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32] of its
+// 32x32 block.  Rows past M or N read the last valid row (results discarded).
+// Requirements (checked by the launcher): K % 128 == 0, 16-byte aligned A, BT.
+#include "device_util.h"
+#include "epilogue.h"
+#include "ie_internal.h"
+
+namespace ie {
+namespace {
+
+constexpr int KG = 128;  // K bytes per group
+
+template <int NB>
+struct Group {
+    i32x4 a[4];
+    i32x4 b[NB][4];
+};
+
+template <int NB>
+__device__ __forceinline__ void load_group(Group<NB>& g, const int8_t* arow,
+                                           const int8_t* const (&brow)[NB], int k0) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) g.a[s] = *reinterpret_cast<const i32x4*>(arow + k0 + 16 * s);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) g.b[j][s] = *reinterpret_cast<const i32x4*>(brow[j] + k0 + 16 * s);
+}
+
+template <int NB>
+__device__ __forceinline__ void mfma_group(const Group<NB>& g, i32x16 (&acc)[NB]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(g.a[s], g.b[j][s], acc[j], 0, 0, 0);
+}
+
+// One wave per workgroup; blockIdx.x walks N blocks fastest so consecutive
+// waves share their A rows in L2.
+template <int EPI, int NB>
+__global__ __launch_bounds__(64) void gemm_i8_stream_kernel(
+    int M, int N, int K, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
+    const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
+    const float* residual, void* C) {
+    const int lane = threadIdx.x;
+    const int r = lane & 31, h = lane >> 5;
+    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32 * NB;
+    const int8_t* arow = A + (size_t)min(m0 + r, M - 1) * K + 64 * h;
+    const int8_t* brow[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) brow[j] = BT + (size_t)min(n0 + 32 * j + r, N - 1) * K + 64 * h;
+
+    i32x16 acc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[j][v] = 0;
+
+    const int ng = K / KG;
+    // Ping-pong over groups: group u+1 (clamped to the last group past the
+    // end, a cache hit) is always in flight while group u runs.  (A four-deep
+    // ring measured slower: a wave load touches 32 rows' cache lines, so the
+    // address path, not latency, is what more requests in flight run into.)
+    Group<NB> ga, gb;
+    load_group(ga, arow, brow, 0);
+    int u = 0;
+    while (true) {
+        load_group(gb, arow, brow, min(u + 1, ng - 1) * KG);
+        mfma_group(ga, acc);
+        if (++u >= ng) break;
+        load_group(ga, arow, brow, min(u + 1, ng - 1) * KG);
+        mfma_group(gb, acc);
+        if (++u >= ng) break;
+    }
+
+    const int cbase = n0 + r;
+    const int rbase = m0 + 4 * h;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int n = cbase + 32 * j;
+        if (n >= N) continue;
+        float sb = 0.0f;
+        if constexpr (EPI != IE_EPI_I32) sb = sB[n];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int m = rbase + 8 * (v >> 2) + (v & 3);
+            if (m < M) {
+                float sa = 0.0f;
+                if constexpr (EPI != IE_EPI_I32) sa = sA[m];
+                store_epilogue<EPI>(C, (size_t)m * N + n, acc[j][v], sa, sb, bias, residual, n);
+            }
+        }
+    }
+}
+
+template <int EPI>
+struct StreamLaunch {
+    static void run(const GemmArgs& a, hipStream_t s) {
+        // Two 32-column blocks per wave once there are enough of them to fill
+        // the GPU several times over; one otherwise.
+        const long long waves2 = (long long)((a.M + 31) / 32) * ((a.N + 63) / 64);
+        if (waves2 >= 1024) {
+            const dim3 grid((a.N + 63) / 64, (a.M + 31) / 32);
+            gemm_i8_stream_kernel<EPI, 2><<<grid, 64, 0, s>>>(
+                a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A),
+                reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
+        } else {
+            const dim3 grid((a.N + 31) / 32, (a.M + 31) / 32);
+            gemm_i8_stream_kernel<EPI, 1><<<grid, 64, 0, s>>>(
+                a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A),
+                reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
+        }
+    }
+};
+
+}  // namespace
+
+bool gemm_i8_stream_applies(const GemmArgs& a) {
+    if (a.K % KG != 0 || a.K == 0) return false;
+    if (((uintptr_t)a.A % 16) || ((uintptr_t)a.BT % 16)) return false;
+    return (a.M + 31) / 32 <= 65535;
+}
+
+void launch_gemm_i8_stream(const GemmArgs& a, hipStream_t s) {
+    if (a.M == 0 || a.N == 0) return;
+    dispatch_epilogue<StreamLaunch>(a.epi, a, s);
+}
+
+}  // namespace ie

@@ -69,6 +69,9 @@ void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s);
 // 256x256-tile MFMA GEMM for large M, N (gemm_i8_mfma256.hip).
 bool gemm_i8_big_applies(const GemmArgs& a);
 void launch_gemm_i8_big(const GemmArgs& a, hipStream_t s);
+// Register-streamed MFMA GEMM for mid-size problems (gemm_i8_stream.hip).
+bool gemm_i8_stream_applies(const GemmArgs& a);
+void launch_gemm_i8_stream(const GemmArgs& a, hipStream_t s);
 // One thread per output; any K % 4 == 0 and any alignment (gemv_i8.hip).
 void launch_gemm_i8_generic(const GemmArgs& a, hipStream_t s);
 constexpr int kGemvMaxM = 16;
