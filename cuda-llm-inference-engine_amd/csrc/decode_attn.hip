@@ -29,7 +29,8 @@
 //     and merge in LDS, so its few chunks load in parallel;
 //   * every split writes its slot, empty ones as (o=0, m=-inf, l=0), so the
 //     merge never reads stale workspace (the reference skips the write).
-// Pass 2 (one wave per (b, query head)) merges the splits with l > 0.  (A
+// Pass 2 (one wave per (b, query head)) merges the splits with l > 0; with a
+// single split pass 1 writes O itself and pass 2 is skipped.  (A
 // "last split to arrive merges" variant needs a device-scope release per
 // workgroup, which on gfx950 writes back the XCD's L2 and cost more than the
 // second launch.)
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(WPS == 1 ? 512 : 64 * WPS) void decode_attn_split_k
     const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
     const int* __restrict__ block_table, const int* __restrict__ context_lens, int H_q,
     int H_kv, int block_size, int nbps, int num_splits, int blocks_per_split, float qscale,
-    float* __restrict__ ws) {
+    float* __restrict__ ws, float* __restrict__ O) {
     constexpr int EPL = D / 16;
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -329,11 +330,21 @@ __global__ __launch_bounds__(WPS == 1 ? 512 : 64 * WPS) void decode_attn_split_k
         }
     }
     // The partial of this split; an empty split writes o = 0, m = -inf, l = 0.
+    // With a single split the partial is the result: O = o / l, written
+    // directly with the merge's arithmetic (a merge of one split has weight
+    // exp2(0) = 1), so no second launch is needed.
     if constexpr (WPS == 1) {
         if (grp == 0) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                float* dst = ws + (((size_t)b * H_q + (size_t)kvh * G + g) * num_splits + split) * (D + 2);
+                const size_t bh = (size_t)b * H_q + (size_t)kvh * G + g;
+                if (num_splits == 1) {
+                    const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) O[bh * D + li * EPL + e] = o[g][e] * inv;
+                    continue;
+                }
+                float* dst = ws + (bh * num_splits + split) * (D + 2);
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) dst[li * EPL + e] = o[g][e];
                 if (li == 0) {
@@ -374,7 +385,12 @@ __global__ __launch_bounds__(WPS == 1 ? 512 : 64 * WPS) void decode_attn_split_k
                     lv = fmaf(sm_l[w][g], f, lv);
                 }
             }
-            float* dst = ws + (((size_t)b * H_q + (size_t)kvh * G + g) * num_splits + split) * (D + 2);
+            const size_t bh = (size_t)b * H_q + (size_t)kvh * G + g;
+            if (num_splits == 1) {
+                O[bh * D + dd] = ov * (lv > 0.0f ? 1.0f / lv : 0.0f);
+                continue;
+            }
+            float* dst = ws + (bh * num_splits + split) * (D + 2);
             dst[dd] = ov;
             if (dd == 0) {
                 dst[D] = mx;
@@ -395,14 +411,18 @@ __global__ __launch_bounds__(256) void decode_attn_merge_kernel(int BH, int num_
 }
 
 // Splits of at least kWaveSplitTokens tokens get one wave each (16+ chunks
-// per wave keep its loads streaming); shorter splits are shared by four waves,
-// which otherwise would walk their few chunks one latency at a time.
+// per wave keep its loads streaming) when there are at least kWaveSplitUnits
+// (b, kv head, split) units to fill the GPU; otherwise four waves share a
+// split, which would else be walked one chunk latency at a time (a handful of
+// units, as in the GPT-2 decode step, needs that parallelism).
 constexpr long long kWaveSplitTokens = 256;
+constexpr long long kWaveSplitUnits = 1024;
 
 template <int D, int G, typename KV>
 void launch_split(const DecodeArgs& a, hipStream_t s) {
     const float qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
-    const bool wave = (long long)a.blocks_per_split * a.block_size >= kWaveSplitTokens;
+    const bool wave = (long long)a.blocks_per_split * a.block_size >= kWaveSplitTokens &&
+                      (long long)a.num_splits * a.H_kv * a.B >= kWaveSplitUnits;
     // One-wave splits: the waves of up to 8 KV heads of the same (b, split)
     // share a workgroup, so the heads' slices of each block (contiguous in
     // the cache row) are read together; measured 5% faster than one wave per
@@ -420,7 +440,7 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
     k<<<grid, wave ? 64 * hw : 256, 0, s>>>(
         a.Q, static_cast<const KV*>(a.k_cache), static_cast<const KV*>(a.v_cache),
         a.block_table, a.context_lens, a.H_q, a.H_kv, a.block_size, a.num_blocks_per_seq,
-        a.num_splits, a.blocks_per_split, qscale, a.workspace);
+        a.num_splits, a.blocks_per_split, qscale, a.workspace, a.O);
 }
 
 template <int D, typename KV>
@@ -439,6 +459,7 @@ void launch_d(const DecodeArgs& a, hipStream_t s) {
         launch_g<D, uint16_t>(a, s);
     else
         launch_g<D, float>(a, s);
+    if (a.num_splits == 1) return;  // the split kernel wrote O
     const int BH = a.B * a.H_q;
     decode_attn_merge_kernel<D><<<(BH + 3) / 4, 256, 0, s>>>(BH, a.num_splits, a.workspace, a.O);
 }

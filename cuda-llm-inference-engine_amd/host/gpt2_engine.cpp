@@ -23,6 +23,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <map>
 #include <numeric>
 #include <random>
 #include <sstream>
@@ -254,14 +255,20 @@ struct GPT2Engine::Impl {
     int *block_table = nullptr, *positions = nullptr, *ctx_lens = nullptr, *tokens = nullptr;
     float* ws = nullptr;
     size_t ws_bytes = 0;
-    int attn_splits = 1, attn_bps = 1;
+    // Attention split plan of the current step (set by run_step): the
+    // max_context_len and split count handed to the split kernel, as
+    // ie_decode_attn would be called with them.
+    struct AttnPlan {
+        int max_ctx = 0, splits = 1;
+    };
+    AttnPlan plan;
     bool fused = false;  // fused step kernels apply to this model
 
     int pos = 0;  // host mirror: tokens in every active sequence
     int* host_tokens = nullptr;  // pinned [max_batch]
 
-    hipGraphExec_t graph = nullptr;
-    int graph_batch = 0;
+    // One captured decode step per (batch, attention split count).
+    std::map<std::pair<int, int>, hipGraphExec_t> graphs;
 
     template <typename T>
     T* dev(size_t count) {
@@ -343,9 +350,6 @@ struct GPT2Engine::Impl {
         const int S = ie_decode_num_splits(cfg.max_seq_len, kBlock, 0);
         ws_bytes = ie_decode_attn_workspace_bytes(B, cfg.n_heads, cfg.d_head, S);
         ws = dev<float>(ws_bytes / sizeof(float));
-        // Split plan of ie_decode_attn for max_context_len = max_seq_len.
-        attn_splits = S;
-        attn_bps = (nbps + S - 1) / S;
         fused = opt.fuse && (cfg.d_head == 64 || cfg.d_head == 128);
         for (int m = 1; m <= B && fused; ++m)
             fused = ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, ie::kEpiQKV) &&
@@ -358,7 +362,8 @@ struct GPT2Engine::Impl {
     }
 
     ~Impl() {  // best effort: a destructor has nowhere to report errors
-        if (graph) (void)hipGraphExecDestroy(graph);
+        for (auto& kv : graphs)
+            if (kv.second) (void)hipGraphExecDestroy(kv.second);
         for (void* p : allocs) (void)hipFree(p);
         if (host_tokens) (void)hipHostFree(host_tokens);
         if (stream) (void)hipStreamDestroy(stream);
@@ -409,7 +414,8 @@ struct GPT2Engine::Impl {
             a.Q = q; a.k_cache = layer_k(l); a.v_cache = layer_v(l); a.kv_dtype = opt.kv_dtype;
             a.block_table = block_table; a.context_lens = ctx_lens;
             a.block_size = kBlock; a.num_blocks_per_seq = nbps;
-            a.num_splits = attn_splits; a.blocks_per_split = attn_bps;
+            a.num_splits = plan.splits;
+            a.blocks_per_split = ((plan.max_ctx + kBlock - 1) / kBlock + plan.splits - 1) / plan.splits;
             a.O = attn; a.workspace = ws;
             ie::launch_decode_attn(a, s);
             IEC(ie::check_launch("decode_attn"));
@@ -453,7 +459,7 @@ struct GPT2Engine::Impl {
                                         layer_v(l), opt.kv_dtype, ctx_lens, s);
             IEC(ie::check_launch("qkv_split_append"));
             IEC(ie_decode_attn(B, H, H, cfg.d_head, q, layer_k(l), layer_v(l), opt.kv_dtype,
-                               block_table, ctx_lens, cfg.max_seq_len, kBlock, nbps, attn, ws, ws_bytes, 0,
+                               block_table, ctx_lens, plan.max_ctx, kBlock, nbps, attn, ws, ws_bytes, plan.splits,
                                st));
             IEC(ie_quantize_fp32_to_int8(B, d, attn, act_q, act_s, st));
             IEC(ie_int8_gemm(B, d, d, act_q, L.out.packed, act_s, L.out.scale, IE_EPI_BIAS_RESIDUAL,
@@ -479,12 +485,26 @@ struct GPT2Engine::Impl {
         IEC(ie::check_launch("advance"));
     }
 
+    // Split plan for a step whose attention sees ctx tokens: one split per
+    // kTokensPerSplit tokens (four waves share a split, so each walks about
+    // six 16-token chunks), at most the workspace's 16; a single split writes
+    // the output directly.  Computed from the host's position mirror, so the
+    // captured graph for that plan can be replayed.
+    static constexpr int kTokensPerSplit = 384;
+    AttnPlan plan_for(int ctx) const {
+        AttnPlan p;
+        p.splits = std::max(1, std::min((ctx + kTokensPerSplit - 1) / kTokensPerSplit, 16));
+        p.max_ctx = p.splits == 16 ? cfg.max_seq_len
+                                   : std::min(p.splits * kTokensPerSplit, cfg.max_seq_len);
+        return p;
+    }
+
     void run_step(int B) {
         if (pos >= cfg.max_seq_len) throw std::runtime_error("context is full (max_seq_len reached)");
+        plan = plan_for(pos + 1);
         if (opt.use_graph) {
-            if (!graph || graph_batch != B) {
-                if (graph) HIPC(hipGraphExecDestroy(graph));
-                graph = nullptr;
+            hipGraphExec_t& graph = graphs[{B, plan.splits}];
+            if (!graph) {
                 hipGraph_t g;
                 HIPC(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
                 try {
@@ -496,9 +516,12 @@ struct GPT2Engine::Impl {
                     throw;
                 }
                 HIPC(hipStreamEndCapture(stream, &g));
-                HIPC(hipGraphInstantiate(&graph, g, nullptr, nullptr, 0));
-                HIPC(hipGraphDestroy(g));
-                graph_batch = B;
+                const hipError_t e = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+                (void)hipGraphDestroy(g);
+                if (e != hipSuccess) {
+                    graph = nullptr;
+                    HIPC(e);
+                }
             }
             HIPC(hipGraphLaunch(graph, stream));
         } else {

@@ -31,6 +31,13 @@ def tiny_dir(tmp_path_factory, ie):
 
 
 @pytest.fixture(scope="module")
+def long_dir(tmp_path_factory, ie):
+    d = tmp_path_factory.mktemp("gpt2_long")
+    ie.write_random_model(d, seed=13, **dict(MID, max_seq_len=1024))
+    return d
+
+
+@pytest.fixture(scope="module")
 def mid_dir(tmp_path_factory, ie):
     d = tmp_path_factory.mktemp("gpt2_mid")
     ie.write_random_model(d, seed=12, **MID)
@@ -207,3 +214,30 @@ def test_fused_graph_replay_and_batch_invariance(ie, mid_dir):
         one = run_steps(ie.Engine(mid_dir, max_batch=1), toks[:, i:i + 1])
         for x, y in zip(a, one):
             assert np.array_equal(x[i], y[0])
+
+
+def test_split_plan_change_past_384_tokens(ie, long_dir):
+    """The engine picks its attention split plan from the context length (one
+    split, written directly, up to 384 tokens; two up to 768 ...) and keeps a
+    captured step per plan.  420 steps cross the switch: the fused and the
+    C ABI steps stay bit-identical, graph replay equals eager execution, and
+    the logits follow the oracle (check_steps)."""
+    from oracle.gpt2_step import OracleGPT2
+
+    B, steps = 2, 420
+    rng = np.random.default_rng(40)
+    toks = rng.integers(0, 1000, (steps, B)).astype(np.int32)
+    fused = ie.Engine(long_dir, max_batch=B)
+    plain = ie.Engine(long_dir, max_batch=B, fuse=False)
+    eager = ie.Engine(long_dir, max_batch=B, use_graph=False)
+    om = OracleGPT2(str(long_dir), batch=B)
+    errs = []
+    for i, t in enumerate(toks):
+        a, b, c = fused.step(t), plain.step(t), eager.step(t)
+        assert np.array_equal(a, b), i
+        assert np.array_equal(a, c), i
+        want = om.step(t)
+        sc = np.abs(want).max()
+        errs.append([np.abs(a[j] - want[j]).max() / sc for j in range(B)])
+    for j in range(B):
+        check_steps([e[j] for e in errs])
