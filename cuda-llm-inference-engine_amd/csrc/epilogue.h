@@ -21,39 +21,57 @@
 
 namespace ie {
 
+// The epilogue value for a float output, from the bias and residual values.
+template <int EPI>
+__device__ __forceinline__ float epilogue_value(int32_t acc, float sa, float sb, float bias_v,
+                                                float res_v) {
+    const float t = (float)acc * sa;
+    if constexpr (EPI == IE_EPI_PLAIN) {
+        return t * sb;
+    } else if constexpr (EPI == IE_EPI_BIAS_GELU) {
+        const float v = fmaf(t, sb, bias_v);
+        const float x3 = v * v * v;
+        const float u = 0.7978845608f * fmaf(0.044715f, x3, v);
+        return 0.5f * v * (1.0f + tanhf(u));
+    } else if constexpr (EPI == IE_EPI_BIAS_RESIDUAL) {
+        return fmaf(t, sb, bias_v) + res_v;
+    } else {  // IE_EPI_BIAS and the routed bias epilogues
+        return fmaf(t, sb, bias_v);
+    }
+}
+
+// Stores one output with its epilogue, the bias and residual values given.
 // NT = true writes C with non-temporal stores: used where C is far larger
 // than the caches (it would otherwise evict the operand panels other
 // workgroups are still reading).
 template <int EPI, bool NT = false>
-__device__ __forceinline__ void store_epilogue(void* C, size_t idx, int32_t acc,
-                                               float sa, float sb,
-                                               const float* bias,
-                                               const float* residual, int n) {
+__device__ __forceinline__ void store_epilogue_v(void* C, size_t idx, int32_t acc, float sa,
+                                                 float sb, float bias_v, float res_v) {
     if constexpr (EPI == IE_EPI_I32) {
         if constexpr (NT)
             __builtin_nontemporal_store(acc, static_cast<int32_t*>(C) + idx);
         else
             static_cast<int32_t*>(C)[idx] = acc;
     } else {
-        const float t = (float)acc * sa;
-        float out;
-        if constexpr (EPI == IE_EPI_PLAIN) {
-            out = t * sb;
-        } else if constexpr (EPI == IE_EPI_BIAS) {
-            out = fmaf(t, sb, bias[n]);
-        } else if constexpr (EPI == IE_EPI_BIAS_GELU) {
-            const float v = fmaf(t, sb, bias[n]);
-            const float x3 = v * v * v;
-            const float u = 0.7978845608f * fmaf(0.044715f, x3, v);
-            out = 0.5f * v * (1.0f + tanhf(u));
-        } else {
-            out = fmaf(t, sb, bias[n]) + residual[idx];
-        }
+        const float out = epilogue_value<EPI>(acc, sa, sb, bias_v, res_v);
         if constexpr (NT)
             __builtin_nontemporal_store(out, static_cast<float*>(C) + idx);
         else
             static_cast<float*>(C)[idx] = out;
     }
+}
+
+// As store_epilogue_v, reading bias[n] and residual[idx] as the epilogue needs.
+template <int EPI, bool NT = false>
+__device__ __forceinline__ void store_epilogue(void* C, size_t idx, int32_t acc,
+                                               float sa, float sb,
+                                               const float* bias,
+                                               const float* residual, int n) {
+    float bias_v = 0.0f, res_v = 0.0f;
+    if constexpr (EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL)
+        bias_v = bias[n];
+    if constexpr (EPI == IE_EPI_BIAS_RESIDUAL) res_v = residual[idx];
+    store_epilogue_v<EPI, NT>(C, idx, acc, sa, sb, bias_v, res_v);
 }
 
 // Runtime-to-compile-time epilogue dispatch.

@@ -28,24 +28,52 @@ namespace {
 constexpr int kRowsPerWG = 16;
 constexpr int kChunk = 128;  // 16-byte columns of A per LDS chunk (2 KiB of K)
 
+// Epilogue operands of one output element (scale of its column, bias,
+// residual), loaded before the dot products so their latency hides behind
+// the weight stream instead of following it.
+struct EpiIn {
+    float sb = 0.0f, bias = 0.0f, res = 0.0f;
+};
+template <int EPI>
+__device__ __forceinline__ EpiIn epi_load(int m, int n, int N, const float* __restrict__ sB,
+                                          const float* bias, const float* residual) {
+    EpiIn e;
+    if constexpr (EPI != IE_EPI_I32) e.sb = sB[n];
+    if constexpr (EPI != IE_EPI_I32 && EPI != IE_EPI_PLAIN) e.bias = bias[n];
+    if constexpr (EPI == IE_EPI_BIAS_RESIDUAL) e.res = residual[(size_t)m * N + n];
+    return e;
+}
+
+// Cache slot of the token each row appends (kEpiQKV): row m writes at
+// positions[m] through its block-table row.  The lookups are wave-uniform
+// (scalar loads), so they wait on nothing but themselves.
+template <int ROWS>
+__device__ __forceinline__ void qkv_slots(const GemvFusion& f, int M, size_t (&slot)[ROWS]) {
+#pragma unroll
+    for (int m = 0; m < ROWS; ++m) {
+        slot[m] = 0;
+        if (m < M) {
+            const int pos = f.positions[m];
+            const int blk = pos / f.block_size;
+            slot[m] = (size_t)f.table[(size_t)m * f.nbps + blk] * f.block_size + (pos - blk * f.block_size);
+        }
+    }
+}
+
 // Output store of every GEMV kernel: the GEMM epilogues, or (kEpiQKV) the
 // bias epilogue routed as the reference's qkv_split + kv_cache_write
-// (src/gpt2_engine.cu:292-315, 321-346) would place it.
+// (src/gpt2_engine.cu:292-315, 321-346) would place it: Q [M, d], K and V at
+// cache slot `slot` of row m, and ctx_lens[m] = positions[m] + 1.
 template <int EPI>
 __device__ __forceinline__ void gemv_store(void* C, int m, int n, int N, int32_t acc, float sa,
-                                           float sb, const float* bias, const float* residual,
-                                           const GemvFusion& f) {
+                                           const EpiIn& e, size_t slot, const GemvFusion& f) {
     if constexpr (EPI == kEpiQKV) {
-        const float v = fmaf((float)acc * sa, sb, bias[n]);
+        const float v = epilogue_value<IE_EPI_BIAS>(acc, sa, e.sb, e.bias, 0.0f);
         const int d = N / 3;
-        const int pos = f.positions[m];
         if (n < d) {
             f.q[(size_t)m * d + n] = v;
-            if (n == 0) f.ctx_lens[m] = pos + 1;
+            if (n == 0) f.ctx_lens[m] = f.positions[m] + 1;
         } else {
-            const int blk = pos / f.block_size;
-            const size_t slot = (size_t)f.table[(size_t)m * f.nbps + blk] * f.block_size +
-                                (pos - blk * f.block_size);
             const bool is_k = n < 2 * d;
             const size_t i = slot * d + (is_k ? n - d : n - 2 * d);
             void* base = is_k ? f.kc : f.vc;
@@ -55,7 +83,7 @@ __device__ __forceinline__ void gemv_store(void* C, int m, int n, int N, int32_t
                 static_cast<float*>(base)[i] = v;
         }
     } else {
-        store_epilogue<EPI>(C, (size_t)m * N + n, acc, sa, sb, bias, residual, n);
+        store_epilogue_v<EPI>(C, (size_t)m * N + n, acc, sa, e.sb, e.bias, e.res);
     }
 }
 
@@ -107,23 +135,23 @@ __device__ __forceinline__ void zero_row(int32_t* dst, float* scale, int lane) {
 // Shared tail: reduce each row's 16 lane partials with DPP and store.
 template <int MT, int EPI>
 __device__ __forceinline__ void gemv_finish(const int32_t (&acc)[MT], int li, int n, bool row_ok,
-                                            int M, int N, const float* sA,
-                                            const float* __restrict__ sB, const float* bias,
-                                            const float* residual, void* C,
+                                            int M, int N, const float* sA, const EpiIn& e,
+                                            const size_t (&slot)[MT], void* C,
                                             const GemvFusion& f) {
     int32_t mine = 0;
+    size_t my_slot = 0;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const int32_t t = row16_sum(acc[m]);
-        if (li == m) mine = t;
+        if (li == m) {
+            mine = t;
+            my_slot = slot[m];
+        }
     }
     if (row_ok && li < M) {
-        float sa = 0.0f, sb = 0.0f;
-        if constexpr (EPI != IE_EPI_I32) {
-            sa = sA[li];
-            sb = sB[n];
-        }
-        gemv_store<EPI>(C, li, n, N, mine, sa, sb, bias, residual, f);
+        float sa = 0.0f;
+        if constexpr (EPI != IE_EPI_I32) sa = sA[li];
+        gemv_store<EPI>(C, li, n, N, mine, sa, e, my_slot, f);
     }
 }
 
@@ -188,8 +216,21 @@ __global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
             }
         }
     };
+    // Epilogue operands of a pass's rows are requested ahead of its weights.
+    EpiIn ein[G];
+    auto load_epi = [&](int r) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            ein[g] = epi_load<EPI>(min(li, M - 1), min(r + g * 4 + (lane >> 4), N - 1), N, sB, bias,
+                                   residual);
+    };
+    size_t slot[MT];
+    if constexpr (EPI == kEpiQKV) qkv_slots<MT>(f, M, slot);
     int r0 = wave_global * (4 * G);
-    if (r0 < N) load_group(r0);
+    if (r0 < N) {
+        load_epi(r0);
+        load_group(r0);
+    }
 
     if constexpr (SRC == kSrcInt8) {
         const i32x4* a4 = reinterpret_cast<const i32x4*>(A);
@@ -230,8 +271,9 @@ __global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int n = r0 + g * 4 + (lane >> 4);
-            gemv_finish<MT, EPI>(acc[g], li, n, n < N, M, N, sa_src, sB, bias, residual, C, f);
+            gemv_finish<MT, EPI>(acc[g], li, n, n < N, M, N, sa_src, ein[g], slot, C, f);
         }
+        if (r0 + step < N) load_epi(r0 + step);
     }
 }
 
@@ -270,7 +312,10 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
             for (int c = li; c < cw; c += 16) dot_chunk<MT>(acc, w[c0 + c], a_lds, kChunk, c);
         }
     }
-    gemv_finish<MT, EPI>(acc, li, n, row_ok, M, N, sA, sB, bias, residual, C, GemvFusion{});
+    const size_t no_slot[MT] = {};
+    gemv_finish<MT, EPI>(acc, li, n, row_ok, M, N, sA,
+                         epi_load<EPI>(min(li, M - 1), row_ok ? n : N - 1, N, sB, bias, residual),
+                         no_slot, C, GemvFusion{});
 }
 
 // 5 <= M <= 16: v_mfma_i32_16x16x64_i8 with the activations (M padded to 16
@@ -312,6 +357,16 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
         else
             return *reinterpret_cast<const i32x4*>(p);
     };
+    // Epilogue operands of this lane's outputs (rows 4 kq + v, column n0 +
+    // col; only wave 0 stores) requested ahead of the weights.
+    EpiIn ein[4];
+    size_t slot[16];
+    if (wave == 0) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            ein[v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(n0 + col, N - 1), N, sB, bias, residual);
+        if constexpr (EPI == kEpiQKV) qkv_slots<16>(f, M, slot);
+    }
     const int8_t* w = BT + (size_t)min(n0 + col, N - 1) * K + kq * 16;
     const int8_t* arow = A + (size_t)min(col, M - 1) * K + kq * 16;  // global A (K > 4096)
     i32x4 wv[U], ag[A_LDS ? 1 : U];
@@ -379,15 +434,19 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
     acc += red[2][lane];
     const int n = n0 + col;
     if (n < N) {
-        float sb = 0.0f;
-        if constexpr (EPI != IE_EPI_I32) sb = sB[n];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int m = 4 * kq + v;
             if (m < M) {
                 float sa = 0.0f;
                 if constexpr (EPI != IE_EPI_I32) sa = sa_src[m];
-                gemv_store<EPI>(C, m, n, N, acc[v], sa, sb, bias, residual, f);
+                size_t sl = 0;
+                if constexpr (EPI == kEpiQKV) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (kq == q) sl = slot[4 * q + v];
+                }
+                gemv_store<EPI>(C, m, n, N, acc[v], sa, ein[v], sl, f);
             }
         }
     }
