@@ -5,6 +5,7 @@ Headline (`value`): INT8 GEMM throughput at M=N=K=8192 (Plain epilogue, int32
 accumulate, fp32 out) in TOP/s, one "step" = one GEMM launch over resident
 inputs.  The same JSON line carries:
   roofline      the 8192^3 kernel against the dense i8 MFMA peak (5.0 POP/s)
+  vendor_gemm   hipBLASLt (torch._int_mm) on the same operands, same box
   gemv          decode-M (1, 4, 16) GEMMs on the GPT-2 weight shapes, the LM
                 head shape and 8192x8192, in GB/s of algorithmic bytes against
                 HBM (8 TB/s), weights rotated through >= 1 GiB of copies so the
@@ -13,8 +14,11 @@ inputs.  The same JSON line carries:
   decode_attn   split-K paged decode attention, BASELINE cfg3 (MHA) and cfg4
                 (GQA, ctx 4096/8192/32768, fp32 and bf16 KV), GB/s of
                 algorithmic bytes against HBM
+  e2e_gpt2      GPT-2 Small decode tok/s (BASELINE cfg5), batch 1 and 16
   cpu_baseline  the C oracle (oracle/liborc.so) on a bounded sample of the
                 8192^3 GEMM, on this host's cores
+  traffic       HBM bytes per launch of the dominant kernels (rocprofv3
+                FETCH_SIZE / WRITE_SIZE passes, calibrated on a 1 GiB copy)
 Kernel durations come from HIP events on the stream the kernels run on.
 """
 import argparse
@@ -44,7 +48,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--skip", default="", help="comma list of gemv,gemm512,attn,cpu,e2e")
+    ap.add_argument("--skip", default="", help="comma list of vendor,gemv,gemm512,attn,cpu,e2e")
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE passes")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
@@ -145,6 +149,33 @@ def bench_headline(ie, steps, warmup):
         "bytes": gemm_bytes(M, N, K),
         "inputs": (Ap, Bp, sA, sB),
     }
+
+
+def bench_vendor(ie, inputs, steps):
+    """hipBLASLt's int8 GEMM (torch._int_mm) on the headline's own quantized
+    operands, timed the same way: a same-box reference point for the
+    power-limited MFMA rate.  It returns int32 with no dequant epilogue (our
+    kernel also writes the fp32 dequant), so it does slightly less work."""
+    import torch
+
+    Ap, Bp, _, _ = inputs
+    M, K = Ap.shape[0], Ap.shape[1] * 4
+    N = Bp.shape[0]
+    A8 = Ap.view(torch.int8).view(M, K)
+    B8 = Bp.view(torch.int8).view(N, K)
+    try:
+        for _ in range(3):
+            C = torch._int_mm(A8, B8.t())
+        torch.cuda.synchronize()
+        with Timer() as t:
+            for _ in range(steps):
+                C = torch._int_mm(A8, B8.t())
+        del C
+    except Exception as e:  # noqa: BLE001 - reported, not fatal
+        return {"error": str(e)[:200]}
+    ms = t.ms / steps
+    return {"library": "hipBLASLt via torch._int_mm (int32 out, no dequant)",
+            "TOP/s": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1), "us": round(ms * 1e3, 1)}
 
 
 # ------------------------------------------------------------------ GEMV
@@ -443,6 +474,9 @@ def main():
                    "M": 8192, "N": 8192, "K": 8192, "parallelism": "none (1 GPU)"},
         "roofline": roof(h["kernel_tops"], PEAK_I8_TOPS, "TOP/s", "mfma"),
     }
+    if "vendor" not in skip:
+        res["vendor_gemm"] = bench_vendor(ie, h["inputs"], args.steps)
+        log(f"vendor {res['vendor_gemm']}")
     if not args.only_headline:
         if "gemv" not in skip:
             res["gemv"] = bench_gemv(ie)
