@@ -182,6 +182,62 @@ int ie_decode_attn(int B, int H_q, int H_kv, int d, const float* Q, const void* 
     return ie::check_launch("decode_attn");
 }
 
+int ie_prefill_attn(int B, int P, int H_q, int H_kv, int d, const float* Q, const void* k_cache,
+                    const void* v_cache, int kv_dtype, const int* block_table, int num_blocks_per_seq,
+                    int block_size, int start_pos, float* O, ie_stream_t stream) {
+    using ie::fail;
+    if (B < 0 || P < 0 || H_q <= 0 || H_kv <= 0 || d <= 0 || start_pos < 0)
+        return fail(IE_ERR_INVALID, "prefill_attn: bad sizes B=%d P=%d H_q=%d H_kv=%d d=%d start=%d", B, P,
+                    H_q, H_kv, d, start_pos);
+    if (H_q % H_kv) return fail(IE_ERR_INVALID, "prefill_attn: H_q=%d not a multiple of H_kv=%d", H_q, H_kv);
+    if (d != 64 && d != 128) return fail(IE_ERR_UNSUPPORTED, "prefill_attn: head dim %d not in {64,128}", d);
+    if (kv_dtype != IE_KV_F32 && kv_dtype != IE_KV_BF16)
+        return fail(IE_ERR_INVALID, "prefill_attn: unknown kv dtype %d", kv_dtype);
+    if (block_size <= 0) return fail(IE_ERR_INVALID, "prefill_attn: block_size=%d", block_size);
+    const long long nb = ((long long)start_pos + P + block_size - 1) / block_size;
+    if (num_blocks_per_seq < nb)
+        return fail(IE_ERR_INVALID, "prefill_attn: num_blocks_per_seq=%d < ceil((start_pos+P)/block_size)=%lld",
+                    num_blocks_per_seq, nb);
+    if (B == 0 || P == 0) return IE_OK;
+    if (!Q || !O || !k_cache || !v_cache || !block_table) return fail(IE_ERR_INVALID, "prefill_attn: null pointer");
+    if (!aligned(Q, 16) || !aligned(O, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+        return fail(IE_ERR_INVALID, "prefill_attn: Q, O and the caches must be 16-byte aligned");
+    if (B > 65535 || H_q > 65535) return fail(IE_ERR_UNSUPPORTED, "prefill_attn: grid too large");
+    ie::PrefillArgs a{};
+    a.B = B; a.P = P; a.H_q = H_q; a.H_kv = H_kv; a.d = d;
+    a.Q = Q; a.k = k_cache; a.v = v_cache; a.kv_dtype = kv_dtype;
+    a.paged = true; a.block_table = block_table; a.num_blocks_per_seq = num_blocks_per_seq;
+    a.block_size = block_size; a.start_pos = start_pos; a.causal = true; a.O = O;
+    ie::launch_prefill_attn(a, (hipStream_t)stream);
+    return ie::check_launch("prefill_attn");
+}
+
+int ie_flash_attn(int B, int H, int N, int d, const float* Q, const float* K, const float* V, float* O,
+                  int causal, ie_stream_t stream) {
+    using ie::fail;
+    if (B < 0 || H <= 0 || N < 0 || d <= 0)
+        return fail(IE_ERR_INVALID, "flash_attn: bad sizes B=%d H=%d N=%d d=%d", B, H, N, d);
+    if (d != 64 && d != 128) return fail(IE_ERR_UNSUPPORTED, "flash_attn: head dim %d not in {64,128}", d);
+    if (B == 0 || N == 0) return IE_OK;
+    if (!Q || !K || !V || !O) return fail(IE_ERR_INVALID, "flash_attn: null pointer");
+    if (!aligned(Q, 16) || !aligned(K, 16) || !aligned(V, 16) || !aligned(O, 16))
+        return fail(IE_ERR_INVALID, "flash_attn: Q, K, V and O must be 16-byte aligned");
+    if (B > 65535 || H > 65535) return fail(IE_ERR_UNSUPPORTED, "flash_attn: grid too large");
+    // O is written while other workgroups still read Q, K and V.
+    const uintptr_t bytes = (uintptr_t)B * H * N * d * sizeof(float);
+    const uintptr_t o0 = (uintptr_t)O, o1 = o0 + bytes;
+    for (const float* in : {Q, K, V}) {
+        const uintptr_t i0 = (uintptr_t)in, i1 = i0 + bytes;
+        if (o0 < i1 && i0 < o1) return fail(IE_ERR_INVALID, "flash_attn: O overlaps Q, K or V");
+    }
+    ie::PrefillArgs a{};
+    a.B = B; a.P = N; a.H_q = H; a.H_kv = H; a.d = d;
+    a.Q = Q; a.k = K; a.v = V; a.kv_dtype = IE_KV_F32;
+    a.paged = false; a.block_size = 1; a.causal = causal != 0; a.O = O;
+    ie::launch_prefill_attn(a, (hipStream_t)stream);
+    return ie::check_launch("flash_attn");
+}
+
 int ie_kv_cache_write(const float* K_src, const float* V_src, void* k_cache, void* v_cache,
                       int kv_dtype, const int* block_table, int seq_len, int start_pos,
                       int n_heads, int d_head, int block_size, ie_stream_t stream) {

@@ -64,6 +64,12 @@ void run_decode_attn(int B, int H_q, int H_kv, int d, const float* Q, const floa
                           workspace, ws, 0, nullptr));
 }
 
+// kernels/flash_attention/10_flash_attn_v2.cuh:7-9
+void run_flash_attn_v2(int B, int H, int N, int d, const float* Q, const float* K, const float* V,
+                       float* O, bool causal) {
+    report("run_flash_attn_v2", ie_flash_attn(B, H, N, d, Q, K, V, O, causal ? 1 : 0, nullptr));
+}
+
 // kernels/layernorm/15_layernorm_residual.cuh (run_layernorm)
 void run_layernorm(int rows, int cols, const float* x, const float* gamma, const float* beta,
                    float* out, float eps) {

@@ -7,7 +7,9 @@
 // current position through its block-table row, and sets the attention
 // context length pos + 1.  advance moves every sequence one position on.
 // Positions and token ids live in device memory, so a captured decode step
-// replays without host involvement.
+// replays without host involvement.  prefill_qkv_write does the same split and
+// append for a prompt chunk (P tokens per sequence, src/gpt2_engine.cu:466-
+// 481 with seq_len = P).
 #include "device_util.h"
 #include "ie_internal.h"
 
@@ -44,6 +46,32 @@ __global__ void advance_kernel(int B, int* __restrict__ positions) {
     if (b < B) positions[b] += 1;
 }
 
+// Prefill: row m = b * P + t of the QKV projection is token t of sequence b,
+// at position start + t.
+template <typename KV>
+__global__ __launch_bounds__(256) void prefill_qkv_write_kernel(
+    int B, int P, int start, int d, const float* __restrict__ qkv, const int* __restrict__ block_table,
+    int nbps, int block_size, float* __restrict__ Q, KV* __restrict__ kc, KV* __restrict__ vc) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)B * P * d) return;
+    const int m = (int)(idx / d), i = (int)(idx - (size_t)m * d);
+    const int b = m / P, pos = start + (m - b * P);
+    const float* row = qkv + (size_t)m * 3 * d;
+    const int blk = pos / block_size;
+    const size_t slot = (size_t)block_table[(size_t)b * nbps + blk] * block_size + (pos - blk * block_size);
+    Q[idx] = row[i];
+    kc[slot * d + i] = to_kv<KV>(row[d + i]);
+    vc[slot * d + i] = to_kv<KV>(row[2 * d + i]);
+}
+
+__global__ void set_positions_kernel(int B, int pos, int* __restrict__ positions, int* __restrict__ ctx_lens) {
+    const int b = blockIdx.x * 64 + threadIdx.x;
+    if (b < B) {
+        positions[b] = pos;
+        ctx_lens[b] = pos;
+    }
+}
+
 }  // namespace
 
 void launch_qkv_split_append(int B, int d, const float* qkv, const int* positions,
@@ -62,6 +90,26 @@ void launch_qkv_split_append(int B, int d, const float* qkv, const int* position
 
 void launch_advance(int B, int* positions, hipStream_t s) {
     advance_kernel<<<(B + 63) / 64, 64, 0, s>>>(B, positions);
+}
+
+void launch_prefill_qkv_write(int B, int P, int start, int d, const float* qkv,
+                              const int* block_table, int nbps, int block_size, float* Q,
+                              void* kc, void* vc, int kv_dtype, hipStream_t s) {
+    const size_t total = (size_t)B * P * d;
+    if (total == 0) return;
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    if (kv_dtype == IE_KV_BF16)
+        prefill_qkv_write_kernel<uint16_t><<<blocks, 256, 0, s>>>(
+            B, P, start, d, qkv, block_table, nbps, block_size, Q, static_cast<uint16_t*>(kc),
+            static_cast<uint16_t*>(vc));
+    else
+        prefill_qkv_write_kernel<float><<<blocks, 256, 0, s>>>(
+            B, P, start, d, qkv, block_table, nbps, block_size, Q, static_cast<float*>(kc),
+            static_cast<float*>(vc));
+}
+
+void launch_set_positions(int B, int pos, int* positions, int* ctx_lens, hipStream_t s) {
+    set_positions_kernel<<<(B + 63) / 64, 64, 0, s>>>(B, pos, positions, ctx_lens);
 }
 
 }  // namespace ie

@@ -94,6 +94,26 @@ struct DecodeArgs {
 };
 void launch_decode_attn(const DecodeArgs& a, hipStream_t s);
 
+// ---- prefill attention (prefill_attn.hip) ----
+// paged: Q/O [B, P, H_q, d], K/V = the paged caches (kv_dtype), query t at
+// position start_pos + t attending to cached positions 0 .. start_pos + t.
+// !paged: Q/K/V/O contiguous fp32 [B, H, P, d] (H_q = H_kv), start_pos 0.
+struct PrefillArgs {
+    int B, P, H_q, H_kv, d;
+    const float* Q;
+    const void* k;
+    const void* v;
+    int kv_dtype;
+    bool paged;
+    const int* block_table;
+    int num_blocks_per_seq;
+    int block_size;
+    int start_pos;
+    bool causal;
+    float* O;
+};
+void launch_prefill_attn(const PrefillArgs& a, hipStream_t s);
+
 // ---- KV cache (kv_cache.hip) ----
 void launch_kv_write(const float* K, const float* V, void* kc, void* vc,
                      int kv_dtype, const int* bt, int seq_len, int start_pos,
@@ -108,6 +128,13 @@ void launch_qkv_split_append(int B, int d, const float* qkv, const int* position
                              const int* block_table, int nbps, int block_size, float* Q,
                              void* kc, void* vc, int kv_dtype, int* ctx_lens, hipStream_t s);
 void launch_advance(int B, int* positions, hipStream_t s);
+// Prefill chunk of P tokens per sequence at positions start .. start+P-1:
+// from QKV rows [B*P, 3d] (row b*P + t) writes Q [B*P, d] and appends K/V.
+void launch_prefill_qkv_write(int B, int P, int start, int d, const float* qkv,
+                              const int* block_table, int nbps, int block_size, float* Q,
+                              void* kc, void* vc, int kv_dtype, hipStream_t s);
+// positions[b] = ctx_lens[b] = pos for every sequence.
+void launch_set_positions(int B, int pos, int* positions, int* ctx_lens, hipStream_t s);
 
 // ---- support ops (support.hip) ----
 void launch_layernorm(int rows, int cols, const float* x, const float* g,

@@ -61,7 +61,8 @@ extern "C" {
 
 int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n_heads, int d_model,
                      int d_ff, int vocab_size, int max_seq_len, unsigned long long seed, int max_batch,
-                     int kv_dtype, int int8_lm_head, int use_graph, int fuse) {
+                     int kv_dtype, int int8_lm_head, int use_graph, int fuse, int prefill,
+                     int prefill_chunk) {
     if (!out) return ie::fail(IE_ERR_INVALID, "ie_engine_create: out is null");
     *out = nullptr;
     GPT2EngineOptions opt;
@@ -70,6 +71,9 @@ int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n
     opt.int8_lm_head = int8_lm_head != 0;
     opt.use_graph = use_graph != 0;
     opt.fuse = fuse != 0;
+    opt.prefill = prefill != 0;
+    opt.prefill_chunk = prefill_chunk;
+    if (prefill_chunk < 0) return ie::fail(IE_ERR_INVALID, "ie_engine_create: prefill_chunk=%d", prefill_chunk);
     return guarded("ie_engine_create", [&] {
         GPT2Engine* e = model_dir ? new GPT2Engine(std::string(model_dir), opt)
                                   : new GPT2Engine(make_cfg(n_layers, n_heads, d_model, d_ff, vocab_size,
@@ -117,26 +121,43 @@ int ie_engine_generate(ie_engine* e, int batch, int prompt_len, const int* promp
     });
 }
 
+namespace {
+// Host copies of the logits [batch, V] left by the last step or prefill, and
+// their first-maximum ids.
+void fetch_logits(GPT2Engine* eng, int batch, float* logits_host, int* argmax_host) {
+    const int V = eng->config().vocab_size;
+    std::vector<float> l;
+    float* dst = logits_host;
+    if (!dst && argmax_host) {
+        l.resize((size_t)batch * V);
+        dst = l.data();
+    }
+    if (!dst) return;
+    hipError_t er = hipMemcpy(dst, eng->logits_device(), sizeof(float) * (size_t)batch * V, hipMemcpyDeviceToHost);
+    if (er != hipSuccess) throw std::runtime_error(hipGetErrorString(er));
+    if (argmax_host)
+        for (int b = 0; b < batch; ++b) {
+            const float* r = dst + (size_t)b * V;
+            argmax_host[b] = (int)(std::max_element(r, r + V) - r);
+        }
+}
+}  // namespace
+
+int ie_engine_prefill(ie_engine* e, int batch, int prompt_len, const int* tokens, float* logits_host,
+                      int* argmax_host) {
+    if (!e || !tokens || batch <= 0 || prompt_len <= 0)
+        return ie::fail(IE_ERR_INVALID, "ie_engine_prefill: bad arguments");
+    return guarded("ie_engine_prefill", [&] {
+        e->eng->prefill(tokens, batch, prompt_len);
+        fetch_logits(e->eng, batch, logits_host, argmax_host);
+    });
+}
+
 int ie_engine_step(ie_engine* e, int batch, const int* tokens, float* logits_host, int* argmax_host) {
     if (!e || !tokens) return ie::fail(IE_ERR_INVALID, "ie_engine_step: bad arguments");
     return guarded("ie_engine_step", [&] {
         e->eng->step(tokens, batch);
-        const int V = e->eng->config().vocab_size;
-        if (logits_host) {
-            hipError_t er = hipMemcpy(logits_host, e->eng->logits_device(), sizeof(float) * (size_t)batch * V,
-                                      hipMemcpyDeviceToHost);
-            if (er != hipSuccess) throw std::runtime_error(hipGetErrorString(er));
-        }
-        if (argmax_host) {
-            std::vector<float> l((size_t)batch * V);
-            hipError_t er = hipMemcpy(l.data(), e->eng->logits_device(), sizeof(float) * l.size(),
-                                      hipMemcpyDeviceToHost);
-            if (er != hipSuccess) throw std::runtime_error(hipGetErrorString(er));
-            for (int b = 0; b < batch; ++b) {
-                const float* r = l.data() + (size_t)b * V;
-                argmax_host[b] = (int)(std::max_element(r, r + V) - r);
-            }
-        }
+        fetch_logits(e->eng, batch, logits_host, argmax_host);
     });
 }
 

@@ -267,6 +267,18 @@ struct GPT2Engine::Impl {
     int pos = 0;  // host mirror: tokens in every active sequence
     int* host_tokens = nullptr;  // pinned [max_batch]
 
+    // Prefill scratch [rows, ...], rows = sequences x chunk tokens, grown on
+    // first use (the decode step never touches it).
+    struct PrefillBufs {
+        int rows = 0;
+        float *x = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr;
+        float* act_s = nullptr;
+        int32_t* act_q = nullptr;
+        int* ids = nullptr;  // pinned host mirror in host_ids
+        int* host_ids = nullptr;
+    } pf;
+    std::vector<void*> pf_allocs;
+
     // One captured decode step per (batch, attention split count).
     std::map<std::pair<int, int>, hipGraphExec_t> graphs;
 
@@ -365,6 +377,8 @@ struct GPT2Engine::Impl {
         for (auto& kv : graphs)
             if (kv.second) (void)hipGraphExecDestroy(kv.second);
         for (void* p : allocs) (void)hipFree(p);
+        for (void* p : pf_allocs) (void)hipFree(p);
+        if (pf.host_ids) (void)hipHostFree(pf.host_ids);
         if (host_tokens) (void)hipHostFree(host_tokens);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -423,15 +437,35 @@ struct GPT2Engine::Impl {
             fused_gemv(B, L.up, ie::kSrcLnQuant, x, L.ln2_g, L.ln2_b, IE_EPI_BIAS_GELU, L.up_b, nullptr, h);
             fused_gemv(B, L.down, ie::kSrcQuant, h, nullptr, nullptr, IE_EPI_BIAS_RESIDUAL, L.down_b, x, x);
         }
-        if (opt.int8_lm_head) {
-            fused_gemv(B, head, ie::kSrcLnQuant, x, lnf_g, lnf_b, IE_EPI_PLAIN, nullptr, nullptr, logits);
-        } else {
-            IEC(ie_layernorm(B, d, x, lnf_g, lnf_b, xn, 1e-5f, (ie_stream_t)s));
-            IEC(ie_vocab_proj(B, xn, wte, logits, d, cfg.vocab_size, (ie_stream_t)s));
-        }
-        IEC(ie_argmax(B, logits, cfg.vocab_size, tokens, (ie_stream_t)s));
+        enqueue_head(B);
         ie::launch_advance(B, positions, s);
         IEC(ie::check_launch("advance"));
+    }
+
+    // Final LayerNorm, LM head and argmax over the hidden rows x [B, d]
+    // (src/gpt2_engine.cu:612-627, 391-410; sampler.cu:10-14): logits
+    // [B, V], argmax ids into `tokens`.
+    void enqueue_head(int B) {
+        const int d = cfg.d_model, V = cfg.vocab_size;
+        ie_stream_t st = (ie_stream_t)stream;
+        if (fused) {
+            if (opt.int8_lm_head) {
+                fused_gemv(B, head, ie::kSrcLnQuant, x, lnf_g, lnf_b, IE_EPI_PLAIN, nullptr, nullptr, logits);
+            } else {
+                IEC(ie_layernorm(B, d, x, lnf_g, lnf_b, xn, 1e-5f, st));
+                IEC(ie_vocab_proj(B, xn, wte, logits, d, V, st));
+            }
+        } else {
+            IEC(ie_layernorm(B, d, x, lnf_g, lnf_b, xn, 1e-5f, st));
+            if (opt.int8_lm_head) {
+                IEC(ie_quantize_fp32_to_int8(B, d, xn, act_q, act_s, st));
+                IEC(ie_int8_gemm(B, V, d, act_q, head.packed, act_s, head.scale, IE_EPI_PLAIN, nullptr, nullptr,
+                                 logits, st));
+            } else {
+                IEC(ie_vocab_proj(B, xn, wte, logits, d, V, st));
+            }
+        }
+        IEC(ie_argmax(B, logits, V, tokens, st));
     }
 
     void enqueue_step(int B) {
@@ -445,7 +479,7 @@ struct GPT2Engine::Impl {
     // leaves logits, writes the argmax into tokens and advances positions.
     // Every operation goes through the public C ABI.
     void enqueue_step_unfused(int B) {
-        const int d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size, H = cfg.n_heads;
+        const int d = cfg.d_model, ff = cfg.d_ff, H = cfg.n_heads;
         hipStream_t s = stream;
         ie_stream_t st = (ie_stream_t)s;
         IEC(ie_embedding_batch(B, tokens, positions, d, wte, wpe, x, st));
@@ -472,15 +506,7 @@ struct GPT2Engine::Impl {
             IEC(ie_int8_gemm(B, d, ff, act_q, L.down.packed, act_s, L.down.scale, IE_EPI_BIAS_RESIDUAL,
                              L.down_b, x, x, st));
         }
-        IEC(ie_layernorm(B, d, x, lnf_g, lnf_b, xn, 1e-5f, st));
-        if (opt.int8_lm_head) {
-            IEC(ie_quantize_fp32_to_int8(B, d, xn, act_q, act_s, st));
-            IEC(ie_int8_gemm(B, V, d, act_q, head.packed, act_s, head.scale, IE_EPI_PLAIN, nullptr, nullptr,
-                             logits, st));
-        } else {
-            IEC(ie_vocab_proj(B, xn, wte, logits, d, V, st));
-        }
-        IEC(ie_argmax(B, logits, V, tokens, st));
+        enqueue_head(B);
         ie::launch_advance(B, positions, s);
         IEC(ie::check_launch("advance"));
     }
@@ -539,6 +565,119 @@ struct GPT2Engine::Impl {
         HIPC(hipStreamSynchronize(stream));
     }
 
+    // ---- prefill ----
+    static constexpr int kPrefillRows = 4096;  // rows (sequences x tokens) per chunk
+
+    bool prefill_applies() const { return opt.prefill && (cfg.d_head == 64 || cfg.d_head == 128); }
+    int prefill_chunk(int B) const {
+        return opt.prefill_chunk > 0 ? opt.prefill_chunk : std::max(1, kPrefillRows / B);
+    }
+
+    void ensure_prefill(int rows) {
+        if (rows <= pf.rows) return;
+        HIPC(hipStreamSynchronize(stream));
+        pf.rows = 0;
+        for (void* p : pf_allocs) (void)hipFree(p);
+        pf_allocs.clear();
+        if (pf.host_ids) (void)hipHostFree(pf.host_ids);
+        pf.host_ids = nullptr;
+        const size_t R = rows, d = cfg.d_model, ff = cfg.d_ff;
+        auto alloc = [&](size_t bytes) {
+            void* p = nullptr;
+            HIPC(hipMalloc(&p, std::max<size_t>(bytes, 16)));
+            pf_allocs.push_back(p);
+            return p;
+        };
+        pf.x = static_cast<float*>(alloc(R * d * 4));
+        pf.xn = static_cast<float*>(alloc(R * d * 4));
+        pf.qkv = static_cast<float*>(alloc(R * 3 * d * 4));
+        pf.q = static_cast<float*>(alloc(R * d * 4));
+        pf.attn = static_cast<float*>(alloc(R * d * 4));
+        pf.h = static_cast<float*>(alloc(R * ff * 4));
+        pf.act_q = static_cast<int32_t*>(alloc(R * std::max(d, ff)));
+        pf.act_s = static_cast<float*>(alloc(R * 4));
+        pf.ids = static_cast<int*>(alloc(R * 4));
+        HIPC(hipHostMalloc(&pf.host_ids, R * sizeof(int)));
+        pf.rows = rows;
+    }
+
+    // A prompt chunk through the model at once (the reference's prefill,
+    // src/gpt2_engine.cu:660-676 with forward_layer's is_prefill branch,
+    // :447-528): B sequences of P tokens (toks[b * P + t]) at positions
+    // pos .. pos + P - 1, as M = B x chunk-row GEMMs and the causal prefill
+    // attention over the paged cache, in chunks of prefill_chunk(B) tokens
+    // per sequence (a later chunk attends to the earlier ones through the
+    // cache).  Every operation goes through the public C ABI.  Leaves the
+    // logits [B, V] of each sequence's last token, their argmax in `tokens`,
+    // and positions at pos + P.  The reference prefills only a fresh session
+    // and feeds a continuation through decode steps; here both prefill.
+    void prefill(const int* toks, int B, int P) {
+        if (B < 1 || B > opt.max_batch) throw std::runtime_error("batch out of range");
+        if (P < 1) throw std::runtime_error("empty prompt");
+        if (!prefill_applies()) throw std::runtime_error("prefill needs d_head 64 or 128");
+        if (pos + P > cfg.max_seq_len) throw std::runtime_error("prompt does not fit the context");
+        const int d = cfg.d_model, ff = cfg.d_ff, H = cfg.n_heads, dh = cfg.d_head;
+        const int chunk = std::min(P, prefill_chunk(B));
+        ensure_prefill(B * chunk);
+        ie_stream_t st = (ie_stream_t)stream;
+        int Pc = 0;
+        for (int c0 = 0; c0 < P; c0 += Pc) {
+            Pc = std::min(chunk, P - c0);
+            const int M = B * Pc;
+            if (c0 > 0) HIPC(hipStreamSynchronize(stream));  // host_ids is about to be rewritten
+            for (int b = 0; b < B; ++b)
+                std::memcpy(pf.host_ids + (size_t)b * Pc, toks + (size_t)b * P + c0, sizeof(int) * Pc);
+            HIPC(hipMemcpyAsync(pf.ids, pf.host_ids, sizeof(int) * M, hipMemcpyHostToDevice, stream));
+            for (int b = 0; b < B; ++b)
+                IEC(ie_embedding(pf.ids + (size_t)b * Pc, Pc, pos, d, wte, wpe, pf.x + (size_t)b * Pc * d, st));
+            for (int l = 0; l < cfg.n_layers; ++l) {
+                const Layer& L = layers[l];
+                IEC(ie_layernorm(M, d, pf.x, L.ln1_g, L.ln1_b, pf.xn, 1e-5f, st));
+                IEC(ie_quantize_fp32_to_int8(M, d, pf.xn, pf.act_q, pf.act_s, st));
+                IEC(ie_int8_gemm(M, 3 * d, d, pf.act_q, L.qkv.packed, pf.act_s, L.qkv.scale, IE_EPI_BIAS, L.qkv_b,
+                                 nullptr, pf.qkv, st));
+                ie::launch_prefill_qkv_write(B, Pc, pos, d, pf.qkv, block_table, nbps, kBlock, pf.q, layer_k(l),
+                                             layer_v(l), opt.kv_dtype, stream);
+                IEC(ie::check_launch("prefill_qkv_write"));
+                IEC(ie_prefill_attn(B, Pc, H, H, dh, pf.q, layer_k(l), layer_v(l), opt.kv_dtype, block_table, nbps,
+                                    kBlock, pos, pf.attn, st));
+                IEC(ie_quantize_fp32_to_int8(M, d, pf.attn, pf.act_q, pf.act_s, st));
+                IEC(ie_int8_gemm(M, d, d, pf.act_q, L.out.packed, pf.act_s, L.out.scale, IE_EPI_BIAS_RESIDUAL,
+                                 L.out_b, pf.x, pf.x, st));
+                IEC(ie_layernorm(M, d, pf.x, L.ln2_g, L.ln2_b, pf.xn, 1e-5f, st));
+                IEC(ie_quantize_fp32_to_int8(M, d, pf.xn, pf.act_q, pf.act_s, st));
+                IEC(ie_int8_gemm(M, ff, d, pf.act_q, L.up.packed, pf.act_s, L.up.scale, IE_EPI_BIAS_GELU, L.up_b,
+                                 nullptr, pf.h, st));
+                IEC(ie_quantize_fp32_to_int8(M, ff, pf.h, pf.act_q, pf.act_s, st));
+                IEC(ie_int8_gemm(M, d, ff, pf.act_q, L.down.packed, pf.act_s, L.down.scale, IE_EPI_BIAS_RESIDUAL,
+                                 L.down_b, pf.x, pf.x, st));
+            }
+            pos += Pc;
+        }
+        // hidden row of each sequence's last token -> x [B, d]
+        HIPC(hipMemcpy2DAsync(x, sizeof(float) * d, pf.x + (size_t)(Pc - 1) * d, sizeof(float) * d * Pc,
+                              sizeof(float) * d, B, hipMemcpyDeviceToDevice, stream));
+        ie::launch_set_positions(B, pos, positions, ctx_lens, stream);
+        IEC(ie::check_launch("set_positions"));
+        enqueue_head(B);
+    }
+
+    // Prompt of B sequences x P tokens through prefill (or, if disabled, one
+    // decode step per position); the argmax ids end up in host_tokens.
+    void run_prompt(const int* toks, int B, int P) {
+        if (prefill_applies()) {
+            prefill(toks, B, P);
+            HIPC(hipMemcpyAsync(host_tokens, tokens, sizeof(int) * B, hipMemcpyDeviceToHost, stream));
+            HIPC(hipStreamSynchronize(stream));
+            return;
+        }
+        std::vector<int> col(B);
+        for (int i = 0; i < P; ++i) {
+            for (int b = 0; b < B; ++b) col[b] = toks[(size_t)b * P + i];
+            step_tokens(col.data(), B, i + 1 == P);
+        }
+    }
+
     double bytes_per_step(int B) const {
         const double d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size;
         double w = cfg.n_layers * (3 * d * d + d * d + 2 * d * ff);          // int8 weights
@@ -591,6 +730,11 @@ const GPT2Config& GPT2Engine::config() const { return impl_->cfg; }
 const float* GPT2Engine::logits_device() const { return impl_->logits; }
 double GPT2Engine::step_bytes(int batch) const { return impl_->bytes_per_step(batch); }
 
+void GPT2Engine::prefill(const int* tokens, int batch, int len) {
+    impl_->prefill(tokens, batch, len);
+    HIPC(hipStreamSynchronize(impl_->stream));
+}
+
 void GPT2Engine::step(const int* tokens, int batch) {
     if (batch < 1 || batch > impl_->opt.max_batch) throw std::runtime_error("batch out of range");
     impl_->step_tokens(tokens, batch, false);
@@ -637,10 +781,9 @@ void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tok
     };
 
     const auto t_total = Clock::now();
-    // Prompt through the decode path, one position per step (what the
-    // reference does for continuation prompts, src/gpt2_engine.cu:680-698).
-    for (size_t i = 0; i < prompt_tokens.size(); ++i)
-        I.step_tokens(&prompt_tokens[i], 1, i + 1 == prompt_tokens.size());
+    // The prompt through prefill (src/gpt2_engine.cu:660-676), or with
+    // prefill off one decode step per position (:680-698).
+    I.run_prompt(prompt_tokens.data(), 1, (int)prompt_tokens.size());
     int next = pick();
     metrics.ttft_ms = ms_since(t_total);
 
@@ -677,12 +820,10 @@ void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, in
     metrics.generating = true;
     I.reset();
     out.assign(B, {});
-    std::vector<int> toks(B);
+    std::vector<int> flat((size_t)B * P);
+    for (int b = 0; b < B; ++b) std::copy(prompts[b].begin(), prompts[b].end(), flat.begin() + (size_t)b * P);
     const auto t_total = Clock::now();
-    for (size_t i = 0; i < P; ++i) {
-        for (int b = 0; b < B; ++b) toks[b] = prompts[b][i];
-        I.step_tokens(toks.data(), B, i + 1 == P);
-    }
+    I.run_prompt(flat.data(), B, (int)P);
     metrics.ttft_ms = ms_since(t_total);
     std::vector<float> itl;
     float decode_ms = 0.0f;

@@ -35,6 +35,8 @@ SIGNATURES = {
     "ie_decode_num_splits": (_I, [_I, _I, _I]),
     "ie_decode_attn_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "ie_decode_attn": (_I, [_I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P, _P, _Z, _I, _P]),
+    "ie_prefill_attn": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P]),
+    "ie_flash_attn": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _I, _P]),
     "ie_kv_cache_write": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P]),
     "ie_kv_cache_append_batch": (_I, [_I, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _P]),
     "ie_layernorm": (_I, [_I, _I, _P, _P, _P, _P, _F, _P]),
@@ -47,12 +49,13 @@ SIGNATURES = {
 # include/ie_engine.h
 ENGINE_SIGNATURES = {
     "ie_engine_create": (_I, [ctypes.POINTER(_P), ctypes.c_char_p, _I, _I, _I, _I, _I, _I,
-                              ctypes.c_ulonglong, _I, _I, _I, _I, _I]),
+                              ctypes.c_ulonglong, _I, _I, _I, _I, _I, _I, _I]),
     "ie_engine_destroy": (_I, [_P]),
     "ie_engine_write_random_model": (_I, [ctypes.c_char_p, _I, _I, _I, _I, _I, _I, ctypes.c_ulonglong]),
     "ie_engine_reset": (_I, [_P]),
     "ie_engine_generate": (_I, [_P, _I, _I, _P, _I, _I, _P, _P]),
     "ie_engine_step": (_I, [_P, _I, _P, _P, _P]),
+    "ie_engine_prefill": (_I, [_P, _I, _I, _P, _P, _P]),
     "ie_engine_session_tokens": (_I, [_P]),
     "ie_engine_config": (_I, [_P, _P]),
     "ie_engine_step_bytes": (ctypes.c_double, [_P, _I]),
@@ -188,6 +191,31 @@ def decode_attn(Q, k_cache, v_cache, block_table, context_lens, max_ctx, block_s
     return out
 
 
+def prefill_attn(Q, k_cache, v_cache, block_table, start_pos, block_size, H_kv, kv_dtype=KV_F32,
+                 out=None, stream=None):
+    """Q [B, P, H_q, d] fp32 (token t at position start_pos + t, its K/V already
+    cached); returns causal O [B, P, H_q, d]."""
+    import torch
+
+    B, P, H_q, d = Q.shape
+    if out is None:
+        out = torch.empty_like(Q)
+    check("ie_prefill_attn", B, P, H_q, H_kv, d, _ptr(Q), _ptr(k_cache), _ptr(v_cache), kv_dtype,
+          _ptr(block_table), block_table.shape[1], block_size, start_pos, _ptr(out), _stream(stream))
+    return out
+
+
+def flash_attn(Q, K, V, causal=True, out=None, stream=None):
+    """Q, K, V [B, H, N, d] fp32 -> O [B, H, N, d] (run_flash_attn_v2)."""
+    import torch
+
+    B, H, N, d = Q.shape
+    if out is None:
+        out = torch.empty_like(Q)
+    check("ie_flash_attn", B, H, N, d, _ptr(Q), _ptr(K), _ptr(V), _ptr(out), int(causal), _stream(stream))
+    return out
+
+
 def kv_cache_write(K, V, k_cache, v_cache, block_table, start_pos, block_size,
                    kv_dtype=KV_F32, stream=None):
     seq, H, dh = K.shape
@@ -256,14 +284,14 @@ class Engine:
     random model of the given shape (GPT-2 Small by default)."""
 
     def __init__(self, model_dir=None, seed=0, max_batch=1, kv_dtype=KV_F32, int8_lm_head=False,
-                 use_graph=True, fuse=True, **cfg):
+                 use_graph=True, fuse=True, prefill=True, prefill_chunk=0, **cfg):
         import numpy as np  # noqa: F401
 
         c = dict(GPT2_SMALL, **cfg)
         h = ctypes.c_void_p()
         check("ie_engine_create", ctypes.byref(h), None if model_dir is None else str(model_dir).encode(),
               c["n_layers"], c["n_heads"], c["d_model"], c["d_ff"], c["vocab_size"], c["max_seq_len"], seed,
-              max_batch, kv_dtype, int(int8_lm_head), int(use_graph), int(fuse))
+              max_batch, kv_dtype, int(int8_lm_head), int(use_graph), int(fuse), int(prefill), prefill_chunk)
         self.h = h
         v = (ctypes.c_int * 7)()
         check("ie_engine_config", h, ctypes.cast(v, ctypes.c_void_p))
@@ -288,6 +316,17 @@ class Engine:
         V = self.cfg["vocab_size"]
         logits = np.empty((B, V), dtype=np.float32) if want_logits else None
         check("ie_engine_step", self.h, B, toks.ctypes.data_as(ctypes.c_void_p),
+              None if logits is None else logits.ctypes.data_as(ctypes.c_void_p), None)
+        return logits
+
+    def prefill(self, tokens, want_logits=True):
+        """tokens [B, P] at the current position -> last-token logits [B, V]."""
+        import numpy as np
+
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        B, P = toks.shape
+        logits = np.empty((B, self.cfg["vocab_size"]), dtype=np.float32) if want_logits else None
+        check("ie_engine_prefill", self.h, B, P, toks.ctypes.data_as(ctypes.c_void_p),
               None if logits is None else logits.ctypes.data_as(ctypes.c_void_p), None)
         return logits
 

@@ -15,6 +15,10 @@
  *                             kernels/quantization/14_int8_gemm.cuh:27-64
  *                             (epilogue = I8Epilogue, 14_int8_gemm.cuh:36)
  *   ie_decode_attn            run_decode_attn  kernels/decode/13_decode_attn.cuh:192-199
+ *   ie_prefill_attn           run_flash_attn_v2 as the engine's prefill uses it
+ *                             (src/gpt2_engine.cu:484-493), over the paged cache
+ *   ie_flash_attn             run_flash_attn_v2
+ *                             kernels/flash_attention/10_flash_attn_v2.cuh:7-9
  *   ie_kv_cache_write         kv_cache_write_kernel / GPT2Engine::kv_cache_append
  *                             src/gpt2_engine.cu:321-346, 431-445
  *   ie_layernorm              run_layernorm  kernels/layernorm/15_layernorm_residual.cu:120-130
@@ -114,6 +118,26 @@ int ie_decode_attn(int B, int H_q, int H_kv, int d, const float* Q,
                    int max_context_len, int block_size, int num_blocks_per_seq,
                    float* O, float* workspace, size_t workspace_bytes,
                    int num_splits, ie_stream_t stream);
+
+/* Causal attention of a prompt chunk over the paged cache: P query tokens per
+ * sequence, token t of sequence b at position start_pos + t, whose K/V (and
+ * those of every earlier position) are already in the cache; each attends to
+ * cached positions 0 .. start_pos + t.  Q and O are token-major
+ * [B, P, H_q, d] fp32 (the QKV projection's layout); caches, block table and
+ * kv_dtype as ie_decode_attn, with start_pos + P <= num_blocks_per_seq *
+ * block_size.  d in {64,128}; H_q a multiple of H_kv. */
+int ie_prefill_attn(int B, int P, int H_q, int H_kv, int d, const float* Q,
+                    const void* k_cache, const void* v_cache, int kv_dtype,
+                    const int* block_table, int num_blocks_per_seq,
+                    int block_size, int start_pos, float* O,
+                    ie_stream_t stream);
+
+/* FlashAttention forward over contiguous fp32 Q, K, V, O [B, H, N, d]
+ * (run_flash_attn_v2, kernels/flash_attention/10_flash_attn_v2.cuh:7-9):
+ * softmax(Q K^T / sqrt(d)) V per (b, h), keys j <= i when causal.  d in
+ * {64,128}; O must not overlap Q, K or V. */
+int ie_flash_attn(int B, int H, int N, int d, const float* Q, const float* K,
+                  const float* V, float* O, int causal, ie_stream_t stream);
 
 /* Writes K/V rows [seq_len, n_heads, d_head] fp32 for positions
  * start_pos..start_pos+seq_len-1 of one sequence into the paged caches

@@ -5,6 +5,7 @@
  *
  *   kernels/quantization/14_int8_gemm.cuh:20-64   quantizer, INT8 GEMM, epilogues
  *   kernels/decode/13_decode_attn.cuh:12,192-199   DA_MAX_SPLITS, run_decode_attn
+ *   kernels/flash_attention/10_flash_attn_v2.cuh   run_flash_attn_v2
  *   kernels/layernorm/15_layernorm_residual.cuh    run_layernorm
  *   kernels/layernorm/15_embed.cuh                 run_embedding
  *
@@ -52,6 +53,12 @@ void run_decode_attn(int B, int H_q, int H_kv, int d, const float* Q,
                      const int* block_table, const int* context_lens,
                      int max_context_len, int block_size,
                      int num_blocks_per_seq, float* O, float* workspace);
+
+/* kernels/flash_attention/10_flash_attn_v2.cuh:7-9: Q, K, V, O [B, H, N, d]
+ * fp32, scale 1/sqrt(d).  d in {64,128}.  O must not overlap Q, K or V (an
+ * overlapping call is reported and leaves O untouched). */
+void run_flash_attn_v2(int B, int H, int N, int d, const float* Q,
+                       const float* K, const float* V, float* O, bool causal);
 
 void run_layernorm(int rows, int cols, const float* x, const float* gamma,
                    const float* beta, float* out, float eps = 1e-5f);

@@ -27,11 +27,13 @@ typedef struct {
 
 /* model_dir != NULL loads the reference on-disk format and ignores the
  * shape arguments; model_dir == NULL builds a random model of that shape.
- * fuse selects the fused decode step (GPT2EngineOptions::fuse). */
+ * fuse selects the fused decode step, prefill / prefill_chunk the prompt path
+ * (GPT2EngineOptions). */
 int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n_heads,
                      int d_model, int d_ff, int vocab_size, int max_seq_len,
                      unsigned long long seed, int max_batch, int kv_dtype,
-                     int int8_lm_head, int use_graph, int fuse);
+                     int int8_lm_head, int use_graph, int fuse, int prefill,
+                     int prefill_chunk);
 int ie_engine_destroy(ie_engine* e);
 int ie_engine_write_random_model(const char* dir, int n_layers, int n_heads, int d_model,
                                  int d_ff, int vocab_size, int max_seq_len,
@@ -45,6 +47,11 @@ int ie_engine_generate(ie_engine* e, int batch, int prompt_len, const int* promp
  * logits [batch, vocab] and of the argmax ids [batch]. */
 int ie_engine_step(ie_engine* e, int batch, const int* tokens, float* logits_host,
                    int* argmax_host);
+/* Prefill of prompt_len tokens per sequence (tokens [batch, prompt_len])
+ * at the current position; optional host copies of the last token's logits
+ * [batch, vocab] and of their argmax ids [batch]. */
+int ie_engine_prefill(ie_engine* e, int batch, int prompt_len, const int* tokens,
+                      float* logits_host, int* argmax_host);
 int ie_engine_session_tokens(ie_engine* e);
 /* cfg[7] = n_layers, n_heads, d_model, d_ff, vocab_size, max_seq_len, d_head. */
 int ie_engine_config(ie_engine* e, int* cfg);

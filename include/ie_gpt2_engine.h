@@ -11,8 +11,9 @@
  * scale,bias}.bin with weights int8x4-packed [N, K/4] and per-row scales [N].
  *
  * Extensions with no reference counterpart: a batch of sequences decoded
- * together (generate_batch), bf16 KV cache, an INT8 LM head, and a decode step
- * captured once as a HIP graph and replayed per token.
+ * together (generate_batch), bf16 KV cache, an INT8 LM head, a decode step
+ * captured once as a HIP graph and replayed per token, and chunked prefill
+ * that also serves continuation prompts.
  */
 #ifndef IE_GPT2_ENGINE_H
 #define IE_GPT2_ENGINE_H
@@ -72,6 +73,11 @@ struct GPT2EngineOptions {
      * the GEMVs and QKV appends to the KV cache in its epilogue (GPT-2
      * widths d = 768, ff = 3072; other shapes use the unfused step). */
     bool fuse = true;
+    /* Prompts run through prefill: M = sequences x tokens GEMMs and a causal
+     * prefill attention over the paged cache (d_head 64 or 128; otherwise, or
+     * when false, one decode step per prompt position). */
+    bool prefill = true;
+    int prefill_chunk = 0; /* tokens per sequence per prefill pass; 0 = 4096 / batch */
 };
 
 class GPT2Engine {
@@ -102,6 +108,11 @@ public:
     void reset_session();
     int session_tokens() const;
     const GPT2Config& config() const;
+
+    /* Prefill of `len` tokens for each of the first `batch` sequences
+     * (tokens[b * len + t]) at the current position; logits of every
+     * sequence's last token are left on the device. */
+    void prefill(const int* tokens, int batch, int len);
 
     /* One decode step for the first `batch` sequences at the current position
      * (tokens on the host); logits of every sequence are left on the device. */

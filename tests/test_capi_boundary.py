@@ -16,7 +16,7 @@ COMPAT = os.path.join(ROOT, "include", "ie_compat.h")
 LIB = os.path.join(PKG, "libie_amd.so")
 
 
-SIGS_EXPECTED = 16  # entry points declared in include/ie_amd.h
+SIGS_EXPECTED = 18  # entry points declared in include/ie_amd.h
 
 
 def declared_c_functions(path=HDR):
@@ -44,7 +44,7 @@ def test_library_loads_and_exports_all(ie):
     # the ctypes tables cover exactly the headers
     assert sorted(ie.SIGNATURES) == names
     eng = declared_c_functions(ENGINE_HDR)
-    assert len(eng) == 9 and sorted(ie.ENGINE_SIGNATURES) == eng
+    assert len(eng) == 10 and sorted(ie.ENGINE_SIGNATURES) == eng
     for n in eng:
         assert hasattr(lib, n), n
     syms = exported()
@@ -120,6 +120,33 @@ def test_decode_attn_validation(ie):
     assert attn(ie, ws=need - 4) == ie.IE_ERR_WORKSPACE
     assert attn(ie, ws=need - 4, ws_ptr=None) == ie.IE_ERR_INVALID
     assert attn(ie, B=0) == ie.IE_OK
+
+
+def prefill(ie, B=2, P=40, H_q=8, H_kv=2, d=128, kvdt=0, nbps=4, bs=16, start=24, Q=FAKE, O=FAKE):
+    return st(ie, "ie_prefill_attn", B, P, H_q, H_kv, d, Q, FAKE, FAKE, kvdt, FAKE, nbps, bs, start, O, None)
+
+
+def test_prefill_attn_validation(ie):
+    assert prefill(ie, d=96) == ie.IE_ERR_UNSUPPORTED
+    assert prefill(ie, H_q=8, H_kv=3) == ie.IE_ERR_INVALID
+    assert prefill(ie, kvdt=2) == ie.IE_ERR_INVALID
+    assert prefill(ie, bs=0) == ie.IE_ERR_INVALID
+    assert prefill(ie, start=-1) == ie.IE_ERR_INVALID
+    assert prefill(ie, nbps=3) == ie.IE_ERR_INVALID       # 24 + 40 tokens need 4 blocks
+    assert prefill(ie, Q=None) == ie.IE_ERR_INVALID
+    assert prefill(ie, O=ctypes.c_void_p((1 << 20) + 8)) == ie.IE_ERR_INVALID
+    assert prefill(ie, P=0) == ie.IE_OK
+    assert prefill(ie, B=0) == ie.IE_OK
+    fa = lambda *a: st(ie, "ie_flash_attn", *a, None)  # noqa: E731
+    assert fa(1, 2, 64, 96, FAKE, FAKE, FAKE, FAKE, 1) == ie.IE_ERR_UNSUPPORTED
+    assert fa(1, 2, 64, 64, FAKE, None, FAKE, FAKE, 1) == ie.IE_ERR_INVALID
+    assert fa(1, 2, -1, 64, FAKE, FAKE, FAKE, FAKE, 1) == ie.IE_ERR_INVALID
+    assert fa(1, 2, 0, 64, FAKE, FAKE, FAKE, FAKE, 1) == ie.IE_OK
+    # O overlapping V (the reference engine's own call passes O = V)
+    base = 1 << 24
+    q, k, v = (ctypes.c_void_p(base + i * (1 << 20)) for i in range(3))
+    assert fa(1, 2, 64, 64, q, k, v, ctypes.c_void_p(base + 2 * (1 << 20) + 256), 1) == ie.IE_ERR_INVALID
+    assert "overlaps" in ie.last_error()
 
 
 def test_split_plan_matches_oracle(ie, orc):

@@ -241,3 +241,106 @@ def test_split_plan_change_past_384_tokens(ie, long_dir):
         errs.append([np.abs(a[j] - want[j]).max() / sc for j in range(B)])
     for j in range(B):
         check_steps([e[j] for e in errs])
+
+
+# ---------------------------------------------------------------- prefill
+def prefill_vs_oracle(ie, model_dir, B, P, steps, seed, eng_kw, orc_kw):
+    """Prefill of a P-token prompt, then decode steps, against the oracle fed
+    the same tokens one position at a time (causal attention over the prompt is
+    the same function either way).  Returns per-sequence error lists: the
+    prefill's last-token logits first, then one per decode step."""
+    from oracle.gpt2_step import OracleGPT2
+
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, 1000, (B, P)).astype(np.int32)
+    toks = rng.integers(0, 1000, (steps, B)).astype(np.int32)
+    eng = ie.Engine(model_dir, max_batch=B, **eng_kw)
+    om = OracleGPT2(str(model_dir), batch=B, **orc_kw)
+    got = eng.prefill(prompt)
+    assert eng.session_tokens() == P
+    for t in range(P):
+        want = om.step(prompt[:, t])
+    errs = []
+    for i in range(steps + 1):
+        if i > 0:
+            got, want = eng.step(toks[i - 1]), om.step(toks[i - 1])
+        sc = np.abs(want).max()
+        errs.append([np.abs(got[b] - want[b]).max() / sc for b in range(B)])
+        for b in range(B):
+            top = np.sort(want[b])[-2:]
+            if top[1] - top[0] > 6e-2 * sc:
+                assert np.argmax(got[b]) == np.argmax(want[b])
+    eng.close()
+    return [[e[b] for e in errs] for b in range(B)]
+
+
+def test_prefill_tiny_matches_oracle(ie, tiny_dir):
+    """128-wide model.  The per-step 2e-3 bar of the decode tests does not
+    hold here: this prompt has an activation within fp32 noise of an int8
+    rounding boundary (the oracle itself, with 1e-7 relative noise on the
+    prompt's attention outputs, moves these logits by up to 7.6e-3 in two of
+    three noise draws), so the bar is check_steps'."""
+    for seq in prefill_vs_oracle(ie, tiny_dir, 2, 30, 10, 50, {}, {}):
+        check_steps(seq)
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_prefill_then_decode_matches_oracle(ie, mid_dir, B):
+    """GPT-2 widths: a 40-token prompt through the M = B x 40 GEMMs and the
+    prefill attention, then 20 decode steps over the cache it wrote."""
+    for seq in prefill_vs_oracle(ie, mid_dir, B, 40, 20, 60 + B, {}, {}):
+        check_steps(seq)
+
+
+def test_prefill_bf16_kv_and_int8_head(ie, mid_dir):
+    for seq in prefill_vs_oracle(ie, mid_dir, 2, 33, 8, 70, dict(kv_dtype=ie.KV_BF16), dict(kv_bf16=True)):
+        check_steps(seq)
+    for seq in prefill_vs_oracle(ie, mid_dir, 2, 33, 8, 71, dict(int8_lm_head=True), dict(int8_lm_head=True)):
+        check_steps(seq)
+
+
+def test_prefill_chunking_and_batch_invariance_bit_exact(ie, mid_dir):
+    """Every prefill row is computed independently of the others: GEMM rows
+    are exact int32 sums with a per-row epilogue, and a query's attention
+    walks the cached keys in an order fixed by their positions.  So a prompt
+    prefilled whole, in 16- or 37-token chunks (each chunk attending to the
+    earlier ones through the cache), or as a batch of one, gives the same bits,
+    and so does the decode step after it."""
+    rng = np.random.default_rng(80)
+    B, P = 3, 100
+    prompt = rng.integers(0, 1000, (B, P)).astype(np.int32)
+    nxt = rng.integers(0, 1000, B).astype(np.int32)
+    runs = []
+    for chunk in (0, 16, 37):
+        eng = ie.Engine(mid_dir, max_batch=B, prefill_chunk=chunk)
+        runs.append((eng.prefill(prompt), eng.step(nxt)))
+        eng.close()
+    for a, b in runs[1:]:
+        assert np.array_equal(runs[0][0], a) and np.array_equal(runs[0][1], b)
+    for i in (0, 2):
+        eng = ie.Engine(mid_dir, max_batch=1)
+        one = eng.prefill(prompt[i:i + 1])
+        assert np.array_equal(one[0], runs[0][0][i])
+        assert np.array_equal(eng.step(nxt[i:i + 1])[0], runs[0][1][i])
+        eng.close()
+
+
+def test_generate_uses_prefill_and_matches_stepwise_prompt(ie, mid_dir):
+    """generate() prefills the prompt; with prefill off it feeds the prompt
+    through decode steps.  Both see the same function of the prompt (first-token
+    logits within the check_steps bar of each other), the prefill one sooner."""
+    rng = np.random.default_rng(90)
+    prompt = rng.integers(0, 1000, (2, 64)).astype(np.int32)
+    a = ie.Engine(mid_dir, max_batch=2)
+    b = ie.Engine(mid_dir, max_batch=2, prefill=False)
+    la = a.prefill(prompt)
+    for t in range(prompt.shape[1]):
+        lb = b.step(prompt[:, t])
+    for r in range(2):
+        assert np.abs(la[r] - lb[r]).max() <= 3e-2 * np.abs(lb[r]).max()
+    a.reset()
+    b.reset()
+    ta, ma = a.generate(prompt, 4, ignore_eos=True)
+    tb, mb = b.generate(prompt, 4, ignore_eos=True)
+    assert a.session_tokens() == b.session_tokens() == 64 + 3
+    assert ma["ttft_ms"] < mb["ttft_ms"]
