@@ -296,7 +296,9 @@ def bench_e2e(ie):
     """GPT-2 Small random-init N(0, 0.02), INT8 per-row
     linears (W8A8 as the reference engine), paged KV, prompt of 128 random ids,
     greedy decode of 256 tokens at batch 1 and 16.  tok/s counts decode steps
-    only (src/gpt2_engine.cu:754); MBU = bytes streamed per step x steps/s / 8 TB/s."""
+    only (src/gpt2_engine.cu:754); MBU = bytes streamed per step x steps/s / 8 TB/s.
+    ttft_ms = prompt prefill + first token; also reported with the prompt fed
+    through decode steps."""
     import numpy as np
 
     out = []
@@ -310,13 +312,25 @@ def bench_e2e(ie):
             eng.generate(prompts, 8, ignore_eos=True)  # warm up (graph capture)
             toks, m = eng.generate(prompts, 256, ignore_eos=True)
             r = {"batch": B, "lm_head": "int8" if head_i8 else "fp32 (reference)",
-                 "step": "fused" if fuse else "unfused",
+                 "step": "fused" if fuse else "unfused", "prompt": "prefill",
                  "decode_tok_s": round(m["tps"], 1), "tpot_ms": round(m["tpot_ms"], 4),
                  "ttft_ms": round(m["ttft_ms"], 2), "itl_p95_ms": round(m["itl_p95_ms"], 4),
                  "mbu": round(m["mbu"], 4), "tokens": int((toks >= 0).sum())}
             out.append(r)
             log(f"e2e {r}")
         eng.close()
+    # time to first token with the prompt fed one decode step per position
+    # (the engine's path with prefill off) for comparison
+    eng = ie.Engine(None, seed=1234, max_batch=16, prefill=False)
+    for B in (1, 16):
+        prompts = rng.integers(0, 50257, (B, 128)).astype(np.int32)
+        eng.generate(prompts, 2, ignore_eos=True)
+        _, m = eng.generate(prompts, 2, ignore_eos=True)
+        r = {"batch": B, "lm_head": "fp32 (reference)", "step": "fused", "prompt": "decode steps",
+             "ttft_ms": round(m["ttft_ms"], 2)}
+        out.append(r)
+        log(f"e2e {r}")
+    eng.close()
     return out
 
 

@@ -476,18 +476,6 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
     store_epilogue<EPI>(C, idx, s, sa, sb, bias, residual, n);
 }
 
-// Compute units of the current device (256 on MI355X), looked up once.
-int num_cus() {
-    static const int n = [] {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-            v = 256;
-        return v;
-    }();
-    return n;
-}
-
 // Weight matrices at least this large are streamed with non-temporal loads
 // (a quarter of the 256 MiB MALL: larger ones do not stay resident anyway).
 constexpr size_t kStreamWeightBytes = 64ull << 20;
@@ -579,6 +567,18 @@ bool vec_ok(const GemmArgs& a) {
 }
 
 }  // namespace
+
+// Compute units of the current device (256 on MI355X), looked up once.
+int num_cus() {
+    static const int n = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            v = 256;
+        return v;
+    }();
+    return n;
+}
 
 void launch_gemv_i8(const GemmArgs& a, hipStream_t s) {
     if (a.M == 0 || a.N == 0) return;

@@ -94,6 +94,9 @@ struct DecodeArgs {
 };
 void launch_decode_attn(const DecodeArgs& a, hipStream_t s);
 
+// Compute units of the current device (gemv_i8.hip).
+int num_cus();
+
 // ---- prefill attention (prefill_attn.hip) ----
 // paged: Q/O [B, P, H_q, d], K/V = the paged caches (kv_dtype), query t at
 // position start_pos + t attending to cached positions 0 .. start_pos + t.

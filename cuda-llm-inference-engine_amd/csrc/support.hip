@@ -2,6 +2,7 @@
 // LayerNorm, token+position embedding, fp32 vocabulary projection and a
 // device-side argmax.  They run once or twice per layer on [M, d] rows, so they
 // are written for low latency, not as roofline kernels.
+#include <algorithm>
 #include <climits>
 
 #include "device_util.h"
@@ -112,6 +113,94 @@ __global__ __launch_bounds__(256) void vocab_proj_kernel(int rows, const float* 
     if (ok && li < rows && li < RT) logits[(size_t)li * V + j] = mine;
 }
 
+// The same projection on v_mfma_f32_16x16x4_f32 for any row count 1..16
+// when d = 256 * NCH (GPT-2: NCH = 3): a 16-vocabulary-row tile of logits^T =
+// wte tile (A) x hidden^T (B, zero past `rows`).
+//   * Persistent workgroups walk the tiles (tile = blockIdx.x + n * gridDim.x)
+//     with the next tile's weights loaded while the current one is computed.
+//   * The four waves split K: wave w owns k in [w d/4, (w+1) d/4), NCH chunks
+//     of 64.  It holds its quarter of the hidden rows in registers for the
+//     whole kernel, so nothing is staged per tile, and its partial 16 x 16
+//     tile is summed with the other three in LDS in a fixed order.
+//   * Within chunk c, load e of lane (i, g) (i = l % 16, g = l / 16) reads
+//     vocabulary row v0 + i at k = 64c + 16e + 4g .. +3, so the four lane
+//     groups of a row read 64 contiguous bytes; MFMA step (e, s) sums
+//     k = 64c + 16e + 4g + s over g for A and B alike, every k once.
+//   * Four accumulators (one per e) keep the MFMAs independent and are added
+//     in a fixed order.
+// A logit depends on its own hidden row only (zero columns add nothing to
+// the others), so a batch of 16 and a batch of 1 give the same bits per row.
+// Plain loads: non-temporal ones measured ~10% slower here.
+template <int NCH>
+__global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const float* __restrict__ h,
+                                                                 const float* __restrict__ wte,
+                                                                 float* __restrict__ logits, int d, int V) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    __shared__ f32x4 red[2][4][64];
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i = lane & 15, g = lane >> 4;
+    const int kq = w * NCH * 64;
+    float4 hb[NCH][4];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            hb[c][e] = i < rows ? *reinterpret_cast<const float4*>(h + (size_t)i * d + kq + 64 * c + 16 * e + 4 * g)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int ntiles = (V + 15) / 16;
+    auto load = [&](float4 (&b)[NCH][4], int t) {
+        const float* p = wte + (size_t)min(min(t, ntiles - 1) * 16 + i, V - 1) * d + kq + 4 * g;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[c][e] = *reinterpret_cast<const float4*>(p + 64 * c + 16 * e);
+    };
+    int par = 0;
+    auto tile = [&](const float4 (&b)[NCH][4], int t) {
+        f32x4 acc[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float4 a = b[c][e], hv = hb[c][e];
+                acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, hv.x, acc[e], 0, 0, 0);
+                acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, hv.y, acc[e], 0, 0, 0);
+                acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, hv.z, acc[e], 0, 0, 0);
+                acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, hv.w, acc[e], 0, 0, 0);
+            }
+        red[par][w][lane] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+        // One barrier per tile: the buffer written here is next written two
+        // tiles later, after every wave has passed the next tile's barrier,
+        // which wave 0 reaches only once it has read this one.
+        __syncthreads();
+        if (w == 0 && i < rows) {
+            const f32x4 s4 = ((red[par][0][lane] + red[par][1][lane]) + red[par][2][lane]) + red[par][3][lane];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int vr = t * 16 + 4 * g + v;  // result row 4g + v, hidden row i
+                if (vr < V) logits[(size_t)i * V + vr] = s4[v];
+            }
+        }
+        par ^= 1;
+    };
+    int t = blockIdx.x;
+    if (t >= ntiles) return;  // uniform over the workgroup
+    float4 wa[NCH][4], wb[NCH][4];
+    load(wa, t);
+    while (true) {
+        load(wb, t + gridDim.x);
+        tile(wa, t);
+        t += gridDim.x;
+        if (t >= ntiles) break;
+        load(wa, t + gridDim.x);
+        tile(wb, t);
+        t += gridDim.x;
+        if (t >= ntiles) break;
+    }
+}
+
 // src/sampler.cu:10-14 on the device: first index of the maximum (ties go to
 // the lower index, as std::max_element).  One 1024-thread workgroup per row;
 // each thread issues 16 independent loads per round (a wave instruction reads
@@ -204,6 +293,19 @@ void launch_embedding_batch(int B, const int* ids, const int* positions, int d,
 void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits, int d, int V,
                        hipStream_t s) {
     if (rows == 0 || V == 0) return;
+    if (d % 256 == 0 && d <= 1280) {
+        // one workgroup per CU: more measured no faster (the stream is
+        // bandwidth-bound with four waves' tiles in flight per CU)
+        const unsigned grid = (unsigned)std::min<long long>((V + 15) / 16, num_cus());
+        switch (d / 256) {
+            case 1: vocab_proj_mfma_kernel<1><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
+            case 2: vocab_proj_mfma_kernel<2><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
+            case 3: vocab_proj_mfma_kernel<3><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
+            case 4: vocab_proj_mfma_kernel<4><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
+            default: vocab_proj_mfma_kernel<5><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
+        }
+        return;
+    }
     const unsigned blocks = (unsigned)((V + 15) / 16);
     if (rows == 1)
         vocab_proj_kernel<1><<<blocks, 256, 0, s>>>(rows, h, wte, logits, d, V);

@@ -112,3 +112,23 @@ def test_embedding_vocab_argmax(ie, orc):
     tie[0, [5, 600]] = 3.0
     tie[1, :] = -1.0
     assert host(ie.argmax(dev(tie))).tolist() == [5, 0]
+
+
+@pytest.mark.parametrize("d,V", [(768, 50257), (128, 1000), (1024, 333), (100, 77)])
+def test_vocab_proj_rows_bit_identical_across_batch(ie, orc, d, V):
+    """Row r of a 16-row projection equals the 1-row and 5-row projections of
+    the same hidden row bit for bit (the engine's batch invariance rests on
+    it), for the MFMA form (d % 64 == 0) and the lane-row form (d = 100); all
+    within 1e-5 of the oracle's fp64 dot products."""
+    r = rng(d + V)
+    wte = (r.standard_normal((V, d)) * 0.02).astype(np.float32)
+    h = r.standard_normal((16, d)).astype(np.float32)
+    wte_d = dev(wte)
+    full = host(ie.vocab_proj(dev(h), wte_d))
+    five = host(ie.vocab_proj(dev(h[:5]), wte_d))
+    assert np.array_equal(full[:5], five)
+    for i in (0, 3, 15):
+        one = host(ie.vocab_proj(dev(h[i:i + 1]), wte_d))
+        assert np.array_equal(one[0], full[i])
+        want = orc.vocab_proj(h[i], wte)
+        assert np.abs(full[i] - want).max() < 1e-5 * np.abs(want).max()
