@@ -23,8 +23,11 @@
 //   * a long split (>= 256 tokens) is one wave: no LDS merge and no barrier
 //     at the end, so a finishing wave never holds up the memory pipeline of
 //     the others (measured ~9% faster than four waves per split at ctx 8192);
-//     the waves of several KV heads of one split share a workgroup so the
-//     heads' slices of a block are fetched together;
+//     the waves of several KV heads share a workgroup so the heads' slices of
+//     a block are fetched together; each wave keeps a ring of chunks in
+//     flight (three for fp32 d = 128), and such launches cut the batch's
+//     chunks into equal workgroup ranges across sequences (balanced kernel
+//     below) instead of one workgroup per (b, split);
 //     a short one is shared by four waves that take its chunks round-robin
 //     and merge in LDS, so its few chunks load in parallel;
 //   * every split writes its slot, empty ones as (o=0, m=-inf, l=0), so the
@@ -34,13 +37,30 @@
 // "last split to arrive merges" variant needs a device-scope release per
 // workgroup, which on gfx950 writes back the XCD's L2 and cost more than the
 // second launch.)
+#include <algorithm>
 #include <cmath>
+#include <map>
+#include <mutex>
 
 #include "device_util.h"
 #include "ie_internal.h"
 
 namespace ie {
 namespace {
+
+// One-wave splits: KV heads (waves) per workgroup at most, and KV chunks per
+// wave in the register ring (R - 1 in flight while one is computed).  The
+// stream is bound by bytes in flight per CU; with d = 128 fp32 a 16-token
+// chunk is 64 VGPRs per lane, so the ring that keeps three chunks in flight
+// only fits at one wave per SIMD (arch VGPRs plus AGPRs), i.e. 4 heads per
+// workgroup: measured 0.676-0.687 of HBM peak at ctx 8192 against 0.634-0.653
+// for 8 heads with a ping-pong pair.  bf16 and d = 64 keep 8 heads and the
+// pair (deeper rings or 32-token bf16 chunks measured slower: the unpacked
+// elements need the registers).
+template <int D, typename KV>
+constexpr int wave_heads() { return D == 128 && sizeof(KV) == 4 ? 4 : 8; }
+template <int D, typename KV>
+constexpr int wave_ring() { return D == 128 && sizeof(KV) == 4 ? 4 : 2; }
 
 // Raw K/V words of one lane's d/16-element slice of one token; bf16 stays
 // packed until use so a prefetched chunk costs half the registers.
@@ -92,23 +112,24 @@ __device__ __forceinline__ void load_q(const float* __restrict__ p, float (&out)
     }
 }
 
-template <int D, typename KV>
+// A chunk of 4T tokens: lane row grp holds tokens c0 + 4j + grp, j < T.
+template <int D, typename KV, int T>
 struct Chunk {
     static constexpr int EPL = D / 16;
-    Slice<EPL, KV> k[4], v[4];
-    bool valid[4];
+    Slice<EPL, KV> k[T], v[T];
+    bool valid[T];
 };
 
-// Loads this lane's slices of tokens c0 + 4j + grp (j < 4) of a 16-token chunk.
-template <int D, typename KV>
-__device__ __forceinline__ void load_chunk(Chunk<D, KV>& c, int c0, int grp, int tok1,
+// Loads this lane's slices of tokens c0 + 4j + grp (j < T) of a chunk.
+template <int D, typename KV, int T>
+__device__ __forceinline__ void load_chunk(Chunk<D, KV, T>& c, int c0, int grp, int tok1,
                                            const int* __restrict__ bt, int block_size,
                                            size_t tok_stride, const KV* kbase, const KV* vbase) {
 // Branch-free: positions past tok1 re-read token tok1-1 (a cache hit) and are
 // masked by `valid`, so the loads never sit in divergent control flow and the
 // compiler can keep the next chunk in flight across the current one.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < T; ++j) {
         const int pos = c0 + 4 * j + grp;
         c.valid[j] = pos < tok1;
         const int pc = min(pos, tok1 - 1);
@@ -119,44 +140,47 @@ __device__ __forceinline__ void load_chunk(Chunk<D, KV>& c, int c0, int grp, int
     }
 }
 
-// Block size 16: all 16 tokens of the chunk (c0 a multiple of 16) lie in
-// physical block `phys`, the same for every lane.
-template <int D, typename KV>
-__device__ __forceinline__ void load_chunk16(Chunk<D, KV>& c, int c0, int grp, int tok1, int phys,
-                                             size_t tok_stride, const KV* kbase, const KV* vbase) {
+// Block size 16: the chunk's tokens (c0 a multiple of 4T) lie in blocks
+// phys[0], phys[1], ... (16 tokens each), the same for every lane.
+template <int D, typename KV, int T>
+__device__ __forceinline__ void load_chunk16(Chunk<D, KV, T>& c, int c0, int grp, int tok1,
+                                             const int (&phys)[(T + 3) / 4], size_t tok_stride,
+                                             const KV* kbase, const KV* vbase) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < T; ++j) {
         const int pos = c0 + 4 * j + grp;
         c.valid[j] = pos < tok1;
         const int pc = min(pos, tok1 - 1);
-        const size_t row = (size_t)phys * 16 + (pc & 15);
+        const size_t row = (size_t)phys[j / 4] * 16 + (pc & 15);
         load_raw(kbase + row * tok_stride, c.k[j]);
         load_raw(vbase + row * tok_stride, c.v[j]);
     }
 }
 
-template <int D, int G, typename KV>
-__device__ __forceinline__ void consume_chunk(const Chunk<D, KV>& c, const float (&q)[G][D / 16],
+template <int D, int G, typename KV, int T>
+__device__ __forceinline__ void consume_chunk(const Chunk<D, KV, T>& c, const float (&q)[G][D / 16],
                                               float (&m)[G], float (&l)[G], float (&o)[G][D / 16]) {
     constexpr int EPL = D / 16;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        float s[4];
+        float s[T];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < T; ++j) {
             float dot = 0.0f;
 #pragma unroll
             for (int e = 0; e < EPL; ++e) dot = fmaf(q[g][e], elem(c.k[j], e), dot);
             dot = row16_sum(dot);
             s[j] = c.valid[j] ? dot : -INFINITY;
         }
-        float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        float cm = s[0];
+#pragma unroll
+        for (int j = 1; j < T; ++j) cm = fmaxf(cm, s[j]);
         cm = max_xor32(max_xor16(cm));
         const float mn = fmaxf(m[g], cm);
         const float alpha = exp2f(m[g] - mn);
-        float p[4], psum = 0.0f;
+        float p[T], psum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < T; ++j) {
             p[j] = exp2f(s[j] - mn);
             psum += p[j];
         }
@@ -165,7 +189,7 @@ __device__ __forceinline__ void consume_chunk(const Chunk<D, KV>& c, const float
         for (int e = 0; e < EPL; ++e) {
             float acc = o[g][e] * alpha;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = fmaf(p[j], elem(c.v[j], e), acc);
+            for (int j = 0; j < T; ++j) acc = fmaf(p[j], elem(c.v[j], e), acc);
             o[g][e] = acc;
         }
         m[g] = mn;
@@ -233,10 +257,107 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ w, int S,
 // WPS waves per split: 4 for short splits (the waves take the split's chunks
 // round-robin and merge in LDS), 1 for long ones (no LDS merge, no barrier).
 // BS16: block_size == 16 (the engine's and the reference's), see below.
+// Partial softmax state (m, l, o) over tokens [tok0, tok1) of sequence b for
+// the G query heads of KV head kvh; the split's WPS waves take its 16-token
+// chunks round-robin (this one is `wave`).  bt is the sequence's block-table
+// row.  On return every lane holds the wave's totals (o summed over the four
+// lane rows).
+template <int D, int G, typename KV, int WPS, bool BS16, int R>
+__device__ __forceinline__ void split_partial(const float* __restrict__ Q, const KV* __restrict__ kcache,
+                                              const KV* __restrict__ vcache, const int* __restrict__ bt,
+                                              int b, int kvh, int H_q, int H_kv, int block_size, int tok0,
+                                              int tok1, int wave, int lane, float qscale, float (&m)[G],
+                                              float (&l)[G], float (&o)[G][D / 16]) {
+    constexpr int EPL = D / 16;
+    // Chunk rows and ring depth: R chunks of 4T tokens cycle through the
+    // registers, R - 1 of them in flight while one is computed.  fp32 with
+    // d = 128 takes 8-token chunks so four fit where two 16-token ones did.
+    constexpr int T = 4;              // lane rows hold T tokens each
+    constexpr int CT = 4 * T;         // tokens per chunk
+    constexpr int STEP = CT * WPS;    // tokens per round of the split's waves
+    const int grp = lane >> 4, li = lane & 15;
+    const size_t tok_stride = (size_t)H_kv * D;
+    const KV* kbase = kcache + (size_t)kvh * D + li * EPL;
+    const KV* vbase = vcache + (size_t)kvh * D + li * EPL;
+
+    // Each wave walks its chunks, keeping the next R - 1 chunks' loads in
+    // flight while it computes the current one.  With block size 16 a chunk
+    // lies in one block, so its physical block id is wave-uniform: it comes
+    // from a scalar load issued one chunk ahead (pn), which does not wait
+    // behind the in-flight KV loads as a vector load would (they retire in
+    // issue order), so the next KV loads go out as soon as a chunk is done.
+    // Chunks past the end re-read the last token (masked), so every step
+    // issues the same loads and the ring needs no branches.
+    Chunk<D, KV, T> buf[R];
+    int c0 = tok0 + wave * CT;
+    constexpr int NPH = (T + 3) / 4;  // blocks per chunk
+    auto phys = [&](int cs) { return bt[min(cs, tok1 - 1) >> 4]; };
+    int pn[NPH];
+    auto prefetch = [&](int cs) {
+#pragma unroll
+        for (int k = 0; k < NPH; ++k) pn[k] = phys(cs + 16 * k);
+    };
+    if constexpr (BS16) prefetch(c0);
+    auto next = [&](Chunk<D, KV, T>& c, int cs) {
+        if constexpr (BS16) {
+            load_chunk16(c, cs, grp, tok1, pn, tok_stride, kbase, vbase);
+            prefetch(cs + STEP);
+        } else {
+            load_chunk(c, cs, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+        }
+    };
+    const bool any = c0 < tok1;
+    if (any) {
+#pragma unroll
+        for (int p = 0; p < R - 1; ++p) next(buf[p], c0 + p * STEP);
+    }
+
+    float q[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        load_q<EPL>(Q + ((size_t)b * H_q + (size_t)kvh * G + g) * D + li * EPL, q[g]);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) q[g][e] *= qscale;
+    }
+
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
+    }
+
+    // Each step issues the chunk R - 1 rounds ahead into the buffer consumed
+    // last, then consumes the current one.
+    if (any) {
+        while (true) {
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                next(buf[(u + R - 1) % R], c0 + (R - 1) * STEP);
+                consume_chunk<D, G, KV, T>(buf[u], q, m, l, o);
+                c0 += STEP;
+                if (c0 >= tok1) goto done;
+            }
+        }
+    }
+done:
+
+    // The four lane rows share the wave's running max: plain sums merge them.
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        l[g] = sum_xor32(sum_xor16(l[g]));
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            o[g][e] = sum_xor32(sum_xor16(o[g][e]));
+        }
+    }
+}
+
 // With WPS == 1 a workgroup holds blockDim.x / 64 waves, one per KV head
 // (kv head = blockIdx.y * waves + wave), all on the same split.
-template <int D, int G, typename KV, int WPS, bool BS16>
-__global__ __launch_bounds__(WPS == 1 ? 512 : 64 * WPS) void decode_attn_split_kernel(
+template <int D, int G, typename KV, int WPS, bool BS16, int R, int NT>
+__global__ __launch_bounds__(NT) void decode_attn_split_kernel(
     const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
     const int* __restrict__ block_table, const int* __restrict__ context_lens, int H_q,
     int H_kv, int block_size, int nbps, int num_splits, int blocks_per_split, float qscale,
@@ -248,7 +369,6 @@ __global__ __launch_bounds__(WPS == 1 ? 512 : 64 * WPS) void decode_attn_split_k
     const int kvh = WPS == 1 ? blockIdx.y * (int)(blockDim.x >> 6) + wid : blockIdx.y;
     const int wave = WPS == 1 ? 0 : wid;
     const int grp = lane >> 4, li = lane & 15;
-    constexpr int STEP = 16 * WPS;  // tokens per round of the split's waves
 
     const int ctx = context_lens[b];
     const long long span = (long long)blocks_per_split * block_size;
@@ -260,75 +380,9 @@ __global__ __launch_bounds__(WPS == 1 ? 512 : 64 * WPS) void decode_attn_split_k
     const int tok1 = (int)min(t0l + span, lim);
 
     const int* bt = block_table + (size_t)b * nbps;
-    const size_t tok_stride = (size_t)H_kv * D;
-    const KV* kbase = kcache + (size_t)kvh * D + li * EPL;
-    const KV* vbase = vcache + (size_t)kvh * D + li * EPL;
-
-    // Each wave walks its chunks of 16 tokens, keeping the next chunk's loads
-    // in flight while it computes the current one.  With block size 16 a
-    // chunk is one block, so its physical block id is wave-uniform: it comes
-    // from a scalar load issued one chunk ahead (phys), which does not wait
-    // behind the in-flight KV loads as a vector load would (they retire in
-    // issue order), so the next KV loads go out as soon as a chunk is done.
-    Chunk<D, KV> ca, cb;
-    int c0 = tok0 + wave * 16;
-    auto phys = [&](int cs) { return bt[min(cs, tok1 - 1) >> 4]; };
-    int pn = 0;
-    if (c0 < tok1) {
-        if constexpr (BS16) {
-            load_chunk16(ca, c0, grp, tok1, phys(c0), tok_stride, kbase, vbase);
-            pn = phys(c0 + STEP);
-        } else {
-            load_chunk(ca, c0, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
-        }
-    }
-    auto next = [&](Chunk<D, KV>& c, int cs) {
-        if constexpr (BS16) {
-            load_chunk16(c, cs, grp, tok1, pn, tok_stride, kbase, vbase);
-            pn = phys(cs + STEP);
-        } else {
-            load_chunk(c, cs, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
-        }
-    };
-
-    float q[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        load_q<EPL>(Q + ((size_t)b * H_q + (size_t)kvh * G + g) * D + li * EPL, q[g]);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) q[g][e] *= qscale;
-    }
-
     float m[G], l[G], o[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
-    }
-
-    // Ping-pong: the loads for chunk c0+STEP are always issued (clamped past
-    // the end) before chunk c0 is consumed.
-    while (c0 < tok1) {
-        next(cb, c0 + STEP);
-        consume_chunk<D, G, KV>(ca, q, m, l, o);
-        c0 += STEP;
-        if (c0 >= tok1) break;
-        next(ca, c0 + STEP);
-        consume_chunk<D, G, KV>(cb, q, m, l, o);
-        c0 += STEP;
-    }
-
-    // The four lane rows share the wave's running max: plain sums merge them.
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        l[g] = sum_xor32(sum_xor16(l[g]));
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            o[g][e] = sum_xor32(sum_xor16(o[g][e]));
-        }
-    }
+    split_partial<D, G, KV, WPS, BS16, R>(Q, kcache, vcache, bt, b, kvh, H_q, H_kv, block_size, tok0, tok1,
+                                       wave, lane, qscale, m, l, o);
     // The partial of this split; an empty split writes o = 0, m = -inf, l = 0.
     // With a single split the partial is the result: O = o / l, written
     // directly with the merge's arithmetic (a merge of one split has weight
@@ -400,6 +454,142 @@ __global__ __launch_bounds__(WPS == 1 ? 512 : 64 * WPS) void decode_attn_split_k
     }
 }
 
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ int wave_incl_scan_i(int v, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+template <int D, int G>
+__device__ __forceinline__ void write_partial(float* __restrict__ dst, const float (&o)[D / 16], float m, float l,
+                                              int li) {
+    constexpr int EPL = D / 16;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) dst[li * EPL + e] = o[e];
+    if (li == 0) {
+        dst[D] = m;
+        dst[D + 1] = l;
+    }
+}
+
+// One-wave splits with a work-balanced partition (used when a launch has
+// many long splits).  With ragged context lengths a (b, split) grid leaves
+// many splits short or empty, so some CUs finish early while others still
+// stream full splits (measured: 67% of HBM peak for lengths U[ctx/2, ctx] at
+// ctx 8192 against 71% for uniform lengths of the same total).  Here the
+// batch's 16-token chunks, sequence after sequence, are cut into gridDim.x
+// equal ranges of q chunks, one per workgroup; a workgroup walks the pieces of
+// the sequences its range covers and writes each piece's partial into slot
+// (its workgroup index - the first workgroup of that sequence).  q is at
+// least ceil(nbmax / (S - 1)) chunks, so a sequence of at most nbmax chunks
+// meets at most S workgroups and its pieces fit the S slots; the workgroup
+// holding a sequence's last piece marks the remaining slots empty (o = 0,
+// m = -inf, l = 0), and an empty sequence's slots are marked by the
+// workgroup its position falls in, so every slot is written exactly once and
+// the merge pass is unchanged.  The partition depends only on the context
+// lengths, so results do not depend on block placement.  Measured at ctx 8192
+// fp32 (four-head workgroups, one per CU): 0.676 of HBM peak against 0.599
+// for the (b, split) grid; bf16 at ctx 32768: 0.684 against 0.625.
+template <int D, int G, typename KV, bool BS16, int R, int NT>
+__global__ __launch_bounds__(NT) void decode_attn_balanced_kernel(
+    const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
+    const int* __restrict__ block_table, const int* __restrict__ context_lens, int B, int H_q,
+    int H_kv, int block_size, int nbps, int num_splits, int nbmax, float qscale,
+    float* __restrict__ ws) {
+    constexpr int EPL = D / 16;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kvh = blockIdx.y * (int)(blockDim.x >> 6) + wid;
+    const int li = lane & 15, grp = lane >> 4;
+    const int W = gridDim.x, w = blockIdx.x;
+    // Tokens of sequence b the kernel may read: its length, clamped to the
+    // table row and to the plan's nbmax chunks.
+    const long long cap = min((long long)nbps * block_size, 16LL * nbmax);
+    auto lim = [&](int b) { return (int)max(0LL, min((long long)context_lens[b], cap)); };
+
+    int C = 0;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+        const int b = b0 + lane;
+        C += wave_sum_i(b < B ? (lim(b) + 15) >> 4 : 0);
+    }
+    const int minq = (nbmax + num_splits - 2) / (num_splits - 1);
+    const int q = max(max((C + W - 1) / W, minq), 1);
+    const int weff = (C + q - 1) / q;  // workgroups with chunks
+    if (w >= max(weff, 1)) return;
+    const int lo = w * q, hi = min(lo + q, C);
+
+    auto empty_slot = [&](int b, int slot) {
+        if (grp != 0) return;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float* dst = ws + (((size_t)b * H_q + (size_t)kvh * G + g) * num_splits + slot) * (D + 2);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) dst[li * EPL + e] = 0.0f;
+            if (li == 0) {
+                dst[D] = -INFINITY;
+                dst[D + 1] = 0.0f;
+            }
+        }
+    };
+
+    // The range covers a contiguous run of sequences: find the first (the
+    // first whose chunks end past lo, or an empty one at or past lo) with a
+    // wave scan, then walk on with scalar state only.
+    int bf = B, pf = C;
+    int base = 0;  // chunks of the sequences before this group of 64
+    for (int b0 = 0; b0 < B; b0 += 64) {
+        const int b = b0 + lane;
+        const int n = b < B ? (lim(b) + 15) >> 4 : 0;
+        const int incl = wave_incl_scan_i(n, lane);
+        const int pre = base + incl - n;
+        const unsigned long long hit = __ballot(b < B && (base + incl > lo || pre >= lo));
+        if (hit) {
+            const int j = __builtin_ctzll(hit);
+            bf = b0 + j;
+            pf = __shfl(pre, j, 64);
+            break;
+        }
+        base += __shfl(incl, 63, 64);
+    }
+    const bool last = w == max(weff, 1) - 1;
+    int pre = __builtin_amdgcn_readfirstlane(pf);
+    for (int bj = __builtin_amdgcn_readfirstlane(bf); bj < B; ++bj) {
+        const int lb = lim(bj);
+        const int post = pre + ((lb + 15) >> 4);
+        // stop at the first sequence starting at or past hi, except the
+        // empty ones at the very end, which belong to the last workgroup
+        if (pre >= hi && !(last && post == pre)) break;
+        if (post == pre) {  // empty sequence
+            for (int slot = 0; slot < num_splits; ++slot) empty_slot(bj, slot);
+        } else {
+            const int seg = w - pre / q;
+            const int tok0 = 16 * (max(lo, pre) - pre);
+            const int tok1 = min(16 * (min(hi, post) - pre), lb);
+            float m[G], l[G], o[G][EPL];
+            split_partial<D, G, KV, 1, BS16, R>(Q, kcache, vcache, block_table + (size_t)bj * nbps, bj, kvh, H_q,
+                                             H_kv, block_size, tok0, tok1, 0, lane, qscale, m, l, o);
+            if (grp == 0 && seg < num_splits) {
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    write_partial<D, G>(ws + (((size_t)bj * H_q + (size_t)kvh * G + g) * num_splits + seg) * (D + 2),
+                                        o[g], m[g], l[g], li);
+            }
+            if (post <= hi)  // the sequence ends here: its later slots are empty
+                for (int slot = seg + 1; slot < num_splits; ++slot) empty_slot(bj, slot);
+        }
+        pre = post;
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void decode_attn_merge_kernel(int BH, int num_splits,
                                                                 const float* __restrict__ ws,
@@ -417,6 +607,23 @@ __global__ __launch_bounds__(256) void decode_attn_merge_kernel(int BH, int num_
 // units, as in the GPT-2 decode step, needs that parallelism).
 constexpr long long kWaveSplitTokens = 256;
 constexpr long long kWaveSplitUnits = 1024;
+// Batches up to this size use the balanced partition for one-wave splits
+// (every workgroup scans the context lengths twice).
+constexpr int kBalancedMaxB = 4096;
+
+// Workgroups of `threads` threads of kernel f resident per CU (at least 1),
+// looked up once per kernel.
+int resident_per_cu(const void* f, int threads) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({f, threads});
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, 0) != hipSuccess || n < 1) n = 1;
+    cache[{f, threads}] = n;
+    return n;
+}
 
 template <int D, int G, typename KV>
 void launch_split(const DecodeArgs& a, hipStream_t s) {
@@ -427,16 +634,40 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
     // share a workgroup, so the heads' slices of each block (contiguous in
     // the cache row) are read together; measured 5% faster than one wave per
     // workgroup at ctx 8192.
-    const int hw = !wave ? 1 : a.H_kv % 8 == 0 ? 8 : a.H_kv % 4 == 0 ? 4 : a.H_kv % 2 == 0 ? 2 : 1;
+    constexpr int HWMAX = wave_heads<D, KV>();
+    constexpr int RW = wave_ring<D, KV>();
+    constexpr int NTW = 64 * HWMAX;
+    int hw = 1;
+    if (wave)
+        for (int c = HWMAX; c >= 1; c >>= 1)
+            if (a.H_kv % c == 0) {
+                hw = c;
+                break;
+            }
     const dim3 grid(a.num_splits, a.H_kv / hw, a.B);
     // Scalar block ids measured 12% faster for bf16 KV at ctx 8192 and 1%
     // slower for fp32 one-wave splits (where the per-lane table loads already
     // sit behind the chunk's own KV loads); fp32 long splits keep those.
     const bool bs16 = a.block_size == 16 && !(wave && sizeof(KV) == 4);
-    auto* k = wave ? (bs16 ? decode_attn_split_kernel<D, G, KV, 1, true>
-                           : decode_attn_split_kernel<D, G, KV, 1, false>)
-                   : (bs16 ? decode_attn_split_kernel<D, G, KV, 4, true>
-                           : decode_attn_split_kernel<D, G, KV, 4, false>);
+    if (wave && a.num_splits >= 2 && a.B <= kBalancedMaxB) {
+        // As many workgroups as are resident at once (occupancy x CUs), so the
+        // equal ranges all run in one round.
+        auto* kb = bs16 ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW>
+                        : decode_attn_balanced_kernel<D, G, KV, false, RW, NTW>;
+        const int gy = a.H_kv / hw;
+        const unsigned W = (unsigned)std::max(1, resident_per_cu((const void*)kb, 64 * hw) * num_cus() / gy);
+        // chunks the plan covers (S x blocks per split, at least max_context_len)
+        const int nbmax = (int)std::min<long long>(((long long)a.num_splits * a.blocks_per_split * a.block_size + 15) / 16,
+                                                   ((long long)a.num_blocks_per_seq * a.block_size + 15) / 16);
+        kb<<<dim3(W, gy), 64 * hw, 0, s>>>(a.Q, static_cast<const KV*>(a.k_cache), static_cast<const KV*>(a.v_cache),
+                                           a.block_table, a.context_lens, a.B, a.H_q, a.H_kv, a.block_size,
+                                           a.num_blocks_per_seq, a.num_splits, nbmax, qscale, a.workspace);
+        return;
+    }
+    auto* k = wave ? (bs16 ? decode_attn_split_kernel<D, G, KV, 1, true, RW, NTW>
+                           : decode_attn_split_kernel<D, G, KV, 1, false, RW, NTW>)
+                   : (bs16 ? decode_attn_split_kernel<D, G, KV, 4, true, 2, 256>
+                           : decode_attn_split_kernel<D, G, KV, 4, false, 2, 256>);
     k<<<grid, wave ? 64 * hw : 256, 0, s>>>(
         a.Q, static_cast<const KV*>(a.k_cache), static_cast<const KV*>(a.v_cache),
         a.block_table, a.context_lens, a.H_q, a.H_kv, a.block_size, a.num_blocks_per_seq,

@@ -210,3 +210,42 @@ def test_reference_sized_workspace(ie, orc):
                               ctx, 16, H, workspace=ws))
     want = orc.decode_attn(Q, kc, vc, table, lens, ctx, 16, H)
     assert rel_err(got, want) < REL
+
+
+@pytest.mark.parametrize("bs", [16, 8])
+@pytest.mark.parametrize("kvdt", [0, 1])
+@pytest.mark.parametrize("d,G", [(64, 1), (128, 4)])
+def test_balanced_partition_ragged_lengths(ie, orc, d, G, kvdt, bs):
+    """Launches with many long one-wave splits cut the batch's chunks into
+    equal workgroup ranges across sequence boundaries.  Ragged lengths from 0
+    to max, more than 64 sequences (two scan groups), 8 split slots."""
+    r = rng(2000 + d + G + kvdt + bs)
+    B, H_kv = 70, 2
+    H_q = H_kv * G
+    lens = r.integers(0, 2049, B)
+    lens[[3, 40]] = 0
+    lens[[5, 66]] = 2048
+    kc, vc, table, _, _ = make_paged_cache(r, B, H_kv, d, lens, bs)
+    Q = r.standard_normal((B, H_q, d)).astype(np.float32)
+    if kvdt:
+        kc, vc = bf16_bits(kc), bf16_bits(vc)
+    want = orc.decode_attn(Q, kc, vc, table, lens, 2048, bs, H_kv, kv_dtype=kvdt)
+    got = run_gpu(ie, Q, kc, vc, table, lens, 2048, bs, H_kv, kv_dtype=kvdt, splits=8)
+    assert rel_err(got, want) < REL
+    assert np.all(got[[3, 40]] == 0)
+
+
+def test_balanced_partition_two_slots_and_invariance(ie, orc):
+    """Two split slots (each sequence meets at most two workgroups), 300
+    sequences; the partition depends on the lengths only, so block placement
+    does not change the bits."""
+    B, H_kv, G, d = 300, 2, 2, 64
+    lens = rng(7).integers(0, 1025, B)
+    kc, vc, table, _, _ = make_paged_cache(rng(8), B, H_kv, d, lens, 16, shuffle=True)
+    kc2, vc2, table2, _, _ = make_paged_cache(rng(8), B, H_kv, d, lens, 16, shuffle=False)
+    Q = rng(9).standard_normal((B, H_kv * G, d)).astype(np.float32)
+    want = orc.decode_attn(Q, kc, vc, table, lens, 1024, 16, H_kv)
+    a = run_gpu(ie, Q, kc, vc, table, lens, 1024, 16, H_kv, splits=2)
+    b = run_gpu(ie, Q, kc2, vc2, table2, lens, 1024, 16, H_kv, splits=2)
+    assert rel_err(a, want) < REL
+    assert np.array_equal(a, b)
