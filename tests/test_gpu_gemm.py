@@ -143,6 +143,31 @@ def test_register_streamed_kernel(ie, orc, M, N, K, epi):
         assert np.array_equal(got, want), np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("M,N,K", [(1100, 2100, 768), (2048, 2304, 768)])
+@pytest.mark.parametrize("epi", [0, 2, 3, 4])
+def test_prefill_sized_wide_gemm(ie, orc, M, N, K, epi):
+    """M >= 1024 with N >= 2048 (a batch of prompts through the QKV / FFN-up
+    projections) runs on the 128x128 LDS tile: ragged M and N, int32 and
+    Plain/Residual bit-exact, GELU to 2e-6."""
+    A, W = problem(M, N, K, 3 * M + N + epi)
+    r = rng(17 + epi)
+    bias = (r.standard_normal(N) * 0.5).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    if epi == 4:
+        got = host(ie.int8_gemm(dev(Ap), dev(Wp), epilogue=ie.EPI_I32, path=ie.PATH_MFMA))
+        assert np.array_equal(got, orc.gemm_i32(Ap, Wp))
+        return
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi,
+                            dev(bias) if epi else None, dev(res) if epi == 3 else None, path=ie.PATH_MFMA))
+    want = orc.gemm(Ap, Wp, sA, sW, epi, bias if epi else None, res if epi == 3 else None)
+    if epi == 2:
+        assert np.allclose(got, want, rtol=2e-6, atol=1e-7), np.abs(got - want).max()
+    else:
+        assert np.array_equal(got, want), np.abs(got - want).max()
+
+
 @pytest.mark.parametrize("path", [1, 2])
 def test_residual_may_alias_output(ie, orc, path):
     import torch
