@@ -20,6 +20,9 @@
 //     whatever order; the int32 result is the K-sum bit for bit.
 // Accumulator v of lane l is C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32] of its
 // 32x32 block.  Rows past M or N read the last valid row (results discarded).
+// When there are few blocks and a long K loop, 2 or 4 waves share a block,
+// each walking a contiguous range of its K-groups, and add their int32 tiles
+// in LDS (exact, so the result is the same bits).
 // Requirements (checked by the launcher): K % 128 == 0, 16-byte aligned A, BT.
 #include "device_util.h"
 #include "epilogue.h"
@@ -56,14 +59,18 @@ __device__ __forceinline__ void mfma_group(const Group<NB>& g, i32x16 (&acc)[NB]
             acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(g.a[s], g.b[j][s], acc[j], 0, 0, 0);
 }
 
-// One wave per workgroup; blockIdx.x walks N blocks fastest so consecutive
-// waves share their A rows in L2.
-template <int EPI, int NB>
-__global__ __launch_bounds__(64) void gemm_i8_stream_kernel(
+// KS waves per workgroup share one C block and split its K-groups into KS
+// contiguous ranges (KS = 1: the whole K loop on one wave); their int32
+// tiles are added in LDS, which is exact, so the result does not depend on
+// KS.  blockIdx.x walks N blocks fastest so consecutive workgroups share
+// their A rows in L2.
+template <int EPI, int NB, int KS>
+__global__ __launch_bounds__(64 * KS) void gemm_i8_stream_kernel(
     int M, int N, int K, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
     const float* residual, void* C) {
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 31, h = lane >> 5;
     const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32 * NB;
     const int8_t* arow = A + (size_t)min(m0 + r, M - 1) * K + 64 * h;
@@ -77,21 +84,39 @@ __global__ __launch_bounds__(64) void gemm_i8_stream_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][v] = 0;
 
-    const int ng = K / KG;
-    // Ping-pong over groups: group u+1 (clamped to the last group past the
-    // end, a cache hit) is always in flight while group u runs.  (A four-deep
-    // ring measured slower: a wave load touches 32 rows' cache lines, so the
-    // address path, not latency, is what more requests in flight run into.)
-    Group<NB> ga, gb;
-    load_group(ga, arow, brow, 0);
-    int u = 0;
-    while (true) {
-        load_group(gb, arow, brow, min(u + 1, ng - 1) * KG);
-        mfma_group(ga, acc);
-        if (++u >= ng) break;
-        load_group(ga, arow, brow, min(u + 1, ng - 1) * KG);
-        mfma_group(gb, acc);
-        if (++u >= ng) break;
+    const int ngt = K / KG;
+    const int g0 = (int)((long long)ngt * wave / KS), g1 = (int)((long long)ngt * (wave + 1) / KS);
+    // Ping-pong over groups: group u+1 (clamped to the last group of the
+    // range, a cache hit) is always in flight while group u runs.  (A
+    // four-deep ring measured slower: a wave load touches 32 rows' cache
+    // lines, so the address path, not latency, is what more requests in
+    // flight run into.)
+    if (g1 > g0) {
+        Group<NB> ga, gb;
+        load_group(ga, arow, brow, g0 * KG);
+        int u = g0;
+        while (true) {
+            load_group(gb, arow, brow, min(u + 1, g1 - 1) * KG);
+            mfma_group(ga, acc);
+            if (++u >= g1) break;
+            load_group(ga, arow, brow, min(u + 1, g1 - 1) * KG);
+            mfma_group(gb, acc);
+            if (++u >= g1) break;
+        }
+    }
+    if constexpr (KS > 1) {
+        // waves 1..KS-1 hand their tiles to wave 0 through LDS
+        __shared__ i32x16 red[KS - 1][NB][64];
+        if (wave > 0) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) red[wave - 1][j][lane] = acc[j];
+        }
+        __syncthreads();
+        if (wave > 0) return;
+#pragma unroll
+        for (int w = 0; w < KS - 1; ++w)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[j] += red[w][j][lane];
     }
 
     const int cbase = n0 + r;
@@ -116,20 +141,30 @@ __global__ __launch_bounds__(64) void gemm_i8_stream_kernel(
 
 template <int EPI>
 struct StreamLaunch {
+    template <int NB, int KS>
+    static void go(const GemmArgs& a, hipStream_t s) {
+        const dim3 grid((a.N + 32 * NB - 1) / (32 * NB), (a.M + 31) / 32);
+        gemm_i8_stream_kernel<EPI, NB, KS><<<grid, 64 * KS, 0, s>>>(
+            a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
+            a.sA, a.sB, a.bias, a.residual, a.C);
+    }
     static void run(const GemmArgs& a, hipStream_t s) {
         // Two 32-column blocks per wave once there are enough of them to fill
-        // the GPU several times over; one otherwise.
+        // the GPU several times over; one otherwise.  With fewer than 1024
+        // blocks, the K-groups are split over 4 waves per block from 16
+        // groups up and over 2 from 4 (M=128: 12.9 -> 9.7 us at K=3072,
+        // N=768; 6.2 -> 5.6 us at K=768; no change at M >= 512).
+        const long long blocks1 = (long long)((a.M + 31) / 32) * ((a.N + 31) / 32);
         const long long waves2 = (long long)((a.M + 31) / 32) * ((a.N + 63) / 64);
+        const int ng = a.K / KG;
         if (waves2 >= 1024) {
-            const dim3 grid((a.N + 63) / 64, (a.M + 31) / 32);
-            gemm_i8_stream_kernel<EPI, 2><<<grid, 64, 0, s>>>(
-                a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A),
-                reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
+            go<2, 1>(a, s);
+        } else if (blocks1 < 1024 && ng >= 16) {
+            go<1, 4>(a, s);
+        } else if (blocks1 < 1024 && ng >= 4) {
+            go<1, 2>(a, s);
         } else {
-            const dim3 grid((a.N + 31) / 32, (a.M + 31) / 32);
-            gemm_i8_stream_kernel<EPI, 1><<<grid, 64, 0, s>>>(
-                a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A),
-                reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
+            go<1, 1>(a, s);
         }
     }
 };

@@ -117,13 +117,15 @@ def test_epilogues(ie, orc, M, K, N, path, epi):
         assert np.array_equal(got, want), np.abs(got - want).max()
 
 
-@pytest.mark.parametrize("M,N,K", [(100, 300, 128), (33, 65, 384), (520, 4100, 256), (1000, 2100, 768)])
+@pytest.mark.parametrize("M,N,K", [(100, 300, 128), (33, 65, 384), (520, 4100, 256), (1000, 2100, 768),
+                                   (128, 768, 3072), (97, 700, 640), (130, 770, 2048)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
 def test_register_streamed_kernel(ie, orc, M, N, K, epi):
     """Mid-size shapes (K % 128 == 0, too few 256x256 tiles for the LDS-tiled
     kernel) run on the register-streamed MFMA kernel: ragged M and N, one and
-    two 32-column blocks per wave (the last two shapes), every epilogue; int32
-    and Plain/Bias/Residual bit-exact, GELU to 2e-6."""
+    two 32-column blocks per wave, K split over 4 waves (128x768x3072,
+    130x770x2048) and 2 waves (97x700x640), every epilogue; int32 and
+    Plain/Bias/Residual bit-exact, GELU to 2e-6."""
     A, W = problem(M, N, K, 7 * M + N + K + epi)
     r = rng(11 + epi)
     bias = (r.standard_normal(N) * 0.5).astype(np.float32)
