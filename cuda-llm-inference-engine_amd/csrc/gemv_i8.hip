@@ -92,15 +92,20 @@ __device__ __forceinline__ void gemv_store(void* C, int m, int n, int N, int32_t
 // LayerNorm), then the per-row quantizer (quant_scale / quant_word, as
 // quant.hip).  So the bytes equal those of the standalone LayerNorm +
 // quantizer pair, and do not depend on M or on which kernel stages the row.
-template <int K, int SRC>
-__device__ __forceinline__ void stage_row(const float* __restrict__ xr, const GemvFusion& f,
-                                          int32_t* dst, float* scale, int lane) {
+// Split into a load phase and a compute phase, so a wave can have several
+// rows' loads in flight before it computes any of them.
+template <int K>
+__device__ __forceinline__ void stage_load(const float* __restrict__ xr, float4 (&v)[K / 256], int lane) {
     static_assert(K % 256 == 0, "a lane stages whole float4s");
-    constexpr int NV = K / 256;
-    float4 v[NV];
     const float4* x4 = reinterpret_cast<const float4*>(xr);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) v[i] = x4[lane + 64 * i];
+    for (int i = 0; i < K / 256; ++i) v[i] = x4[lane + 64 * i];
+}
+
+template <int K, int SRC>
+__device__ __forceinline__ void stage_compute(float4 (&v)[K / 256], const GemvFusion& f, int32_t* dst,
+                                              float* scale, int lane) {
+    constexpr int NV = K / 256;
     if constexpr (SRC == kSrcLnQuant) {
         float s = 0.0f, s2 = 0.0f, mean, rs;
 #pragma unroll
@@ -122,6 +127,14 @@ __device__ __forceinline__ void stage_row(const float* __restrict__ xr, const Ge
 #pragma unroll
     for (int i = 0; i < NV; ++i) dst[lane + 64 * i] = quant_word(v[i], inv);
     if (lane == 0) *scale = sc;
+}
+
+template <int K, int SRC>
+__device__ __forceinline__ void stage_row(const float* __restrict__ xr, const GemvFusion& f,
+                                          int32_t* dst, float* scale, int lane) {
+    float4 v[K / 256];
+    stage_load<K>(xr, v, lane);
+    stage_compute<K, SRC>(v, f, dst, scale, lane);
 }
 
 // Rows m >= M of a fused prologue: zero bytes (their outputs are not stored).
@@ -384,12 +397,27 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
                 a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)mm * K)[i - m * (K / 16)];
             }
         } else {
-            for (int m = wave; m < 16; m += 4) {
-                int32_t* dst = reinterpret_cast<int32_t*>(a_lds + m * (K / 16));
-                if (m < M)
-                    stage_row<K, SRC>(f.x + (size_t)m * K, f, dst, &s_sa[m], lane);
-                else
-                    zero_row<K>(dst, &s_sa[m], lane);
+            // Wave w builds rows w, w + 4, w + 8, w + 12: RB rows' loads go out
+            // together (4 at K <= 1024, 2 at larger K for registers), so the
+            // rows cost one memory round trip per batch, not one each.
+            constexpr int RB = K <= 1024 ? 4 : 2;
+#pragma unroll
+            for (int m0 = 0; m0 < 16; m0 += 4 * RB) {
+                float4 v[RB][K / 256];
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    const int m = m0 + 4 * r + wave;
+                    if (m < M) stage_load<K>(f.x + (size_t)m * K, v[r], lane);
+                }
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    const int m = m0 + 4 * r + wave;
+                    int32_t* dst = reinterpret_cast<int32_t*>(a_lds + m * (K / 16));
+                    if (m < M)
+                        stage_compute<K, SRC>(v[r], f, dst, &s_sa[m], lane);
+                    else
+                        zero_row<K>(dst, &s_sa[m], lane);
+                }
             }
         }
         __syncthreads();
