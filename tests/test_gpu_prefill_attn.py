@@ -129,3 +129,59 @@ def test_flash_attn_contiguous(ie, orc, N, d, causal):
                           causal=causal).transpose(0, 2, 1, 3)
     got = host(ie.flash_attn(dev(Q), dev(K), dev(V), causal=causal))
     assert rel_err(got, want) < REL
+
+
+K10_CASES = [(1, 1, 128, 64), (1, 12, 128, 64), (1, 12, 256, 64), (1, 12, 512, 64), (2, 12, 256, 64)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("case", K10_CASES)
+def test_reference_k10_cases(ie, orc, case, causal):
+    """The reference's own FlashAttention tests (tests/test_attention.cu:82-109,
+    156-159 and the multi-batch case): srand(42), Q, K, V drawn interleaved per
+    element as rand()/RAND_MAX*2-1 in [B, H, N, d], max |O - O_ref| < 1e-5
+    (:93, :109); here also within 1e-5 of the output scale."""
+    B, H, N, d = case
+    u = orc.GlibcRand(42).uniform(3 * B * H * N * d)
+    Q = np.ascontiguousarray(u[0::3].reshape(B, H, N, d))
+    K = np.ascontiguousarray(u[1::3].reshape(B, H, N, d))
+    V = np.ascontiguousarray(u[2::3].reshape(B, H, N, d))
+    kc = np.ascontiguousarray(K.transpose(0, 2, 1, 3))
+    vc = np.ascontiguousarray(V.transpose(0, 2, 1, 3))
+    table = np.arange(B, dtype=np.int32).reshape(B, 1)
+    want = oracle_prefill(orc, np.ascontiguousarray(Q.transpose(0, 2, 1, 3)), kc, vc, table, 0, N, H,
+                          causal=causal).transpose(0, 2, 1, 3)
+    got = host(ie.flash_attn(dev(Q), dev(K), dev(V), causal=causal))
+    assert np.abs(got - want).max() < 1e-5
+    assert rel_err(got, want) < REL
+
+
+K12_CASES = [(1, 8, 8, 128), (1, 8, 4, 128), (1, 8, 2, 128), (1, 16, 4, 256), (1, 8, 1, 128), (2, 8, 4, 128)]
+
+
+@pytest.mark.parametrize("case", K12_CASES)
+def test_reference_gqa_paged_cases(ie, orc, case):
+    """The reference's paged GQA prefill tests (tests/test_paged_attention.cu:
+    184-284, causal cases): srand(42), Q [B, H_q, N, d] drawn first, then K and V
+    [B, H_kv, N, d] interleaved per element, block size 16, identity block table,
+    max |O - O_ref| < 1e-5.  Q and O are token-major here (transposed)."""
+    B, H_q, H_kv, N = case
+    d, bs = 64, 16
+    g = orc.GlibcRand(42)
+    Qh = g.uniform(B * H_q * N * d).reshape(B, H_q, N, d)
+    K, V = g.uniform_pair(B * H_kv * N * d)
+    K = K.reshape(B, H_kv, N, d)
+    V = V.reshape(B, H_kv, N, d)
+    nbps = (N + bs - 1) // bs
+    kc = np.zeros((B * nbps, bs, H_kv, d), np.float32)
+    vc = np.zeros_like(kc)
+    for b in range(B):
+        for t in range(N):
+            kc[b * nbps + t // bs, t % bs] = K[b, :, t]
+            vc[b * nbps + t // bs, t % bs] = V[b, :, t]
+    table = np.arange(B * nbps, dtype=np.int32).reshape(B, nbps)
+    Q = np.ascontiguousarray(Qh.transpose(0, 2, 1, 3))  # [B, N, H_q, d]
+    want = oracle_prefill(orc, Q, kc, vc, table, 0, bs, H_kv)
+    got = host(ie.prefill_attn(dev(Q), dev(kc), dev(vc), dev(table), 0, bs, H_kv))
+    assert np.abs(got - want).max() < 1e-5
+    assert rel_err(got, want) < REL
