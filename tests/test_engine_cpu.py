@@ -42,3 +42,22 @@ def test_writer_rejects_bad_config(ie, tmp_path):
     assert st == ie.IE_ERR_INVALID  # d_head = 128 / 3 is not an integer head size
     st = ie.call("ie_engine_write_random_model", str(tmp_path / "y").encode(), 2, 4, 128, 256, 100, 64, 1)
     assert st == ie.IE_ERR_INVALID and "d_head" in ie.last_error()  # d_head 32 unsupported
+
+
+def test_engine_c_api_rejects_bad_arguments_without_a_gpu(ie):
+    """The engine's C entry points validate on the host: null handles, empty
+    prompts and bad option values fail with a status before any HIP call."""
+    import ctypes
+
+    lib = ie.load()
+    P = ctypes.c_void_p
+    assert lib.ie_engine_prefill(None, 1, 4, P(1 << 20), None, None) == ie.IE_ERR_INVALID
+    toks = (ctypes.c_int * 4)(1, 2, 3, 4)
+    assert lib.ie_engine_prefill(None, 1, 4, ctypes.cast(toks, P), None, None) == ie.IE_ERR_INVALID
+    assert lib.ie_engine_step(None, 1, ctypes.cast(toks, P), None, None) == ie.IE_ERR_INVALID
+    assert lib.ie_engine_generate(None, 1, 4, ctypes.cast(toks, P), 2, 0, None, None) == ie.IE_ERR_INVALID
+    h = P()
+    # negative prefill chunk
+    st = lib.ie_engine_create(ctypes.byref(h), None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, -5)
+    assert st == ie.IE_ERR_INVALID and "prefill_chunk" in ie.last_error()
+    assert lib.ie_engine_create(None, None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, 0) == ie.IE_ERR_INVALID
