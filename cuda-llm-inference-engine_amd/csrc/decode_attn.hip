@@ -220,31 +220,36 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ w, int S,
     for (int s0 = 0; s0 < S; s0 += 64) {
         const int s = s0 + lane;
         float f = 0.0f;
+        bool on = false;
         if (s < S) {
             const float* p = w + (size_t)s * (D + 2);
             const float ls = p[D + 1];
-            f = ls > 0.0f ? exp2f(p[D] - mx) : 0.0f;
+            on = ls > 0.0f;
+            f = on ? exp2f(p[D] - mx) : 0.0f;
             l = fmaf(ls, f, l);
         }
+        // Splits with l > 0; an empty one (l = 0, whose o the balanced pass
+        // does not write) reads split s0's row instead (a cache hit) and adds
+        // 0, so its own o is never touched.
+        const unsigned long long live = __ballot(on);
         const int cnt = min(64, S - s0);
         const float* p0 = w + (size_t)s0 * (D + 2) + lane;
         for (int jb = 0; jb < cnt; jb += 8) {
-            // Eight splits' o rows in flight; indices past cnt re-read the
-            // last one and are masked.
+            // Eight splits' o rows in flight, branch-free; their addresses
+            // depend only on the scalar mask, so the loads go out at once.
             float pv[8][PER];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int j = min(jb + u, cnt - 1);
+                const int j = (live >> (jb + u)) & 1ull ? jb + u : 0;
 #pragma unroll
                 for (int i = 0; i < PER; ++i) pv[u][i] = p0[(size_t)j * (D + 2) + 64 * i];
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
+                const bool lv = (live >> (jb + u)) & 1ull;
                 const float fj = __shfl(f, (jb + u) & 63, 64);
-                if (jb + u < cnt) {
 #pragma unroll
-                    for (int i = 0; i < PER; ++i) o[i] = fmaf(pv[u][i], fj, o[i]);
-                }
+                for (int i = 0; i < PER; ++i) o[i] = fmaf(lv ? pv[u][i] : 0.0f, lv ? fj : 0.0f, o[i]);
             }
         }
     }
@@ -492,8 +497,8 @@ __device__ __forceinline__ void write_partial(float* __restrict__ dst, const flo
 // (its workgroup index - the first workgroup of that sequence).  q is at
 // least ceil(nbmax / (S - 1)) chunks, so a sequence of at most nbmax chunks
 // meets at most S workgroups and its pieces fit the S slots; the workgroup
-// holding a sequence's last piece marks the remaining slots empty (o = 0,
-// m = -inf, l = 0), and an empty sequence's slots are marked by the
+// holding a sequence's last piece marks the remaining slots empty (m = -inf,
+// l = 0), and an empty sequence's slots are marked by the
 // workgroup its position falls in, so every slot is written exactly once and
 // the merge pass is unchanged.  The partition depends only on the context
 // lengths, so results do not depend on block placement.  Measured at ctx 8192
@@ -527,17 +532,15 @@ __global__ __launch_bounds__(NT) void decode_attn_balanced_kernel(
     if (w >= max(weff, 1)) return;
     const int lo = w * q, hi = min(lo + q, C);
 
+    // An empty slot needs only (m = -inf, l = 0): the merge gives it weight 0
+    // and never reads its o.
     auto empty_slot = [&](int b, int slot) {
-        if (grp != 0) return;
+        if (lane != 0) return;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float* dst = ws + (((size_t)b * H_q + (size_t)kvh * G + g) * num_splits + slot) * (D + 2);
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) dst[li * EPL + e] = 0.0f;
-            if (li == 0) {
-                dst[D] = -INFINITY;
-                dst[D + 1] = 0.0f;
-            }
+            dst[D] = -INFINITY;
+            dst[D + 1] = 0.0f;
         }
     };
 
