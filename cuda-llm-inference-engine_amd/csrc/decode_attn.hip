@@ -56,11 +56,31 @@ namespace {
 // workgroup: measured 0.676-0.687 of HBM peak at ctx 8192 against 0.634-0.653
 // for 8 heads with a ping-pong pair.  bf16 and d = 64 keep 8 heads and the
 // pair (deeper rings or 32-token bf16 chunks measured slower: the unpacked
-// elements need the registers).
-template <int D, typename KV>
-constexpr int wave_heads() { return D == 128 && sizeof(KV) == 4 ? 4 : 8; }
-template <int D, typename KV>
-constexpr int wave_ring() { return D == 128 && sizeof(KV) == 4 ? 4 : 2; }
+// elements need the registers).  G = 8 at d = 128 holds 8 heads' q and o per
+// wave, so it takes 4 waves per workgroup (one per SIMD, all registers) and
+// the pair: at 8 waves, or with a four-chunk fp32 ring, it spilled and ran at
+// 0.15-0.25 of HBM peak against 0.52-0.66 (fp32) and 0.35-0.40 (bf16) now,
+// ctx 4096-32768 (a three-chunk bf16 ring measured 7% slower).
+template <int D, typename KV, int G>
+constexpr int wave_heads() { return (D == 128 && sizeof(KV) == 4) || (D == 128 && G == 8) ? 4 : 8; }
+template <int D, typename KV, int G>
+constexpr int wave_ring() { return D == 128 && sizeof(KV) == 4 && G < 8 ? 4 : 2; }
+
+template <typename T>
+using global_ptr = __attribute__((address_space(1))) const T*;
+
+// The same global address with its provenance hidden from alias analysis.
+// Loads through a const __restrict__ kernel argument count as invariant, and
+// the compiler sinks invariant loads past the ring's exit branches into the
+// step that consumes them, which turns the ring into issue-all-then-drain.
+// Loads through the returned pointer stay where they are written (and stay
+// global loads: the address space survives the round trip).
+template <typename T>
+__device__ __forceinline__ const T* opaque_global(const T* p) {
+    global_ptr<T> g = (global_ptr<T>)p;
+    asm volatile("" : "+s"(g));
+    return (const T*)g;
+}
 
 // Raw K/V words of one lane's d/16-element slice of one token; bf16 stays
 // packed until use so a prefetched chunk costs half the registers.
@@ -259,6 +279,183 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ w, int S,
     for (int i = 0; i < PER; ++i) out[lane + 64 * i] = o[i] * inv;
 }
 
+// fp32 d = 128 one-wave splits with the K half of each chunk landed in LDS
+// (global_load_lds_dwordx4, 16 bytes per lane straight into a per-wave ring
+// slot) and the V half in registers.  The ring stays at R = 4 chunks, R - 1
+// in flight: a fifth keeps 80 vector-memory operations outstanding, past
+// vmcnt's 63, and the compiler then drains the counter to zero.  What the LDS
+// buys is register room: no K copies, and the V loads stay where they are
+// issued (opaque_global), so the ring streams instead of issuing three chunks
+// at once and draining; measured 0.67 / 0.69-0.72 / 0.78 of HBM peak at ctx
+// 4096 / 8192 / 32768 against 0.64 / 0.67-0.69 / 0.77 for the register ring
+// (same boxes, 32 x 32/8 heads, ragged).  Lane (grp, li) loads K of token
+// c0 + 4j + grp, elements 8 li .. 8 li + 7, as two 16-byte pieces into piece
+// 2j + h of the slot at lane * 16, and reads back exactly the bytes it loaded.
+// Ordering (the compiler does not see the LDS reads, which are inline asm,
+// so it neither drains the ring before them nor knows they wait on the DMA):
+//   * a chunk's K copies are issued before its V loads (a scheduling barrier
+//     keeps that order) and vector memory operations retire in order, so once
+//     the chunk's last V load has landed its K is in LDS; the K read takes
+//     that V register as an input operand, which makes the compiler wait for
+//     it first;
+//   * the read waits for its own LDS results before returning, and a slot is
+//     refilled only by a later step, after the read.
+// Block size 16 only (block ids by scalar loads, no vector table loads).
+constexpr int kKldsRing = 4;
+typedef __attribute__((address_space(3))) void* klds_ptr_t;
+typedef __attribute__((address_space(1))) void* kgbl_ptr_t;
+
+template <int G, int NW>
+__device__ __forceinline__ void split_partial_klds(const float* __restrict__ Q, const float* __restrict__ kcache,
+                                                   const float* __restrict__ vcache, const int* __restrict__ bt,
+                                                   int b, int kvh, int H_q, int H_kv, int tok0, int tok1, int lane,
+                                                   float qscale, float (&m)[G], float (&l)[G], float (&o)[G][8]) {
+    constexpr int D = 128, EPL = 8, T = 4, R = kKldsRing, STEP = 16;
+    // [wave][slot][piece][lane] 16-byte pieces: 8 KB per slot
+    __shared__ __attribute__((aligned(16))) float4 kring[NW][R][2 * T][64];
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane >> 4, li = lane & 15;
+    tok0 = __builtin_amdgcn_readfirstlane(tok0);
+    tok1 = __builtin_amdgcn_readfirstlane(tok1);
+    const size_t tok_stride = (size_t)H_kv * D;
+    const float* kbase = kcache + (size_t)kvh * D + li * EPL;
+    const float* vbase = opaque_global(vcache) + (size_t)kvh * D + li * EPL;
+
+    float q[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        load_q<EPL>(Q + ((size_t)b * H_q + (size_t)kvh * G + g) * D + li * EPL, q[g]);
+
+    struct VChunk {
+        float4 v[T][2];
+        bool valid[T];
+    };
+    VChunk buf[R];
+    int c0 = tok0;
+    // the chunk's block id is wave-uniform: a scalar load, counted by lgkmcnt
+    auto phys = [&](int cs) { return bt[__builtin_amdgcn_readfirstlane(min(cs, tok1 - 1) >> 4)]; };
+    int pn = phys(c0);
+    // Issues chunk cs: K pieces into ring slot `slot`, then V into vb.
+    auto issue = [&](VChunk& vb, int slot, int cs) {
+        const int ph = pn;
+        pn = phys(cs + STEP);
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+            const int pos = cs + 4 * j + grp;
+            const int pc = min(pos, tok1 - 1);
+            const float* kp = kbase + ((size_t)ph * 16 + (pc & 15)) * tok_stride;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                __builtin_amdgcn_global_load_lds((kgbl_ptr_t)(kp + 4 * h), (klds_ptr_t)&kring[wv][slot][2 * j + h][0],
+                                                 16, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+            const int pos = cs + 4 * j + grp;
+            vb.valid[j] = pos < tok1;
+            const int pc = min(pos, tok1 - 1);
+            const float4* vp = reinterpret_cast<const float4*>(vbase + ((size_t)ph * 16 + (pc & 15)) * tok_stride);
+            vb.v[j][0] = vp[0];
+            vb.v[j][1] = vp[1];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const bool any = c0 < tok1;
+    if (any) {
+#pragma unroll
+        for (int p = 0; p < R - 1; ++p) issue(buf[p], p, c0 + p * STEP);
+    }
+
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) q[g][e] *= qscale;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
+    }
+
+    auto consume = [&](const VChunk& vb, int slot) {
+        // K of this chunk from LDS, after its last V load has landed
+        float4 kv[T][2];
+        const unsigned base = (unsigned)(uintptr_t)&kring[wv][slot][0][lane];
+        asm volatile(
+            "ds_read_b128 %0, %8\n\t"
+            "ds_read_b128 %1, %8 offset:1024\n\t"
+            "ds_read_b128 %2, %8 offset:2048\n\t"
+            "ds_read_b128 %3, %8 offset:3072\n\t"
+            "ds_read_b128 %4, %8 offset:4096\n\t"
+            "ds_read_b128 %5, %8 offset:5120\n\t"
+            "ds_read_b128 %6, %8 offset:6144\n\t"
+            "ds_read_b128 %7, %8 offset:7168\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(kv[0][0]), "=&v"(kv[0][1]), "=&v"(kv[1][0]), "=&v"(kv[1][1]), "=&v"(kv[2][0]), "=&v"(kv[2][1]),
+              "=&v"(kv[3][0]), "=&v"(kv[3][1])
+            : "v"(base), "v"(vb.v[T - 1][1].w)
+            : "memory");
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float sc[T];
+#pragma unroll
+            for (int j = 0; j < T; ++j) {
+                const float kk[8] = {kv[j][0].x, kv[j][0].y, kv[j][0].z, kv[j][0].w,
+                                     kv[j][1].x, kv[j][1].y, kv[j][1].z, kv[j][1].w};
+                float dot = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) dot = fmaf(q[g][e], kk[e], dot);
+                dot = row16_sum(dot);
+                sc[j] = vb.valid[j] ? dot : -INFINITY;
+            }
+            float cm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            cm = max_xor32(max_xor16(cm));
+            const float mn = fmaxf(m[g], cm);
+            const float alpha = exp2f(m[g] - mn);
+            float p[T], psum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < T; ++j) {
+                p[j] = exp2f(sc[j] - mn);
+                psum += p[j];
+            }
+            l[g] = fmaf(l[g], alpha, psum);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                float acc = o[g][e] * alpha;
+#pragma unroll
+                for (int j = 0; j < T; ++j) {
+                    const float4 vv = vb.v[j][e >> 2];
+                    const float ve = (e & 3) == 0 ? vv.x : (e & 3) == 1 ? vv.y : (e & 3) == 2 ? vv.z : vv.w;
+                    acc = fmaf(p[j], ve, acc);
+                }
+                o[g][e] = acc;
+            }
+            m[g] = mn;
+        }
+    };
+    if (any) {
+        while (true) {
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                issue(buf[(u + R - 1) % R], (u + R - 1) % R, c0 + (R - 1) * STEP);
+                consume(buf[u], u);
+                c0 += STEP;
+                if (c0 >= tok1) goto done;
+            }
+        }
+    }
+done:
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        l[g] = sum_xor32(sum_xor16(l[g]));
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] = sum_xor32(sum_xor16(o[g][e]));
+    }
+}
+
 // WPS waves per split: 4 for short splits (the waves take the split's chunks
 // round-robin and merge in LDS), 1 for long ones (no LDS merge, no barrier).
 // BS16: block_size == 16 (the engine's and the reference's), see below.
@@ -282,8 +479,12 @@ __device__ __forceinline__ void split_partial(const float* __restrict__ Q, const
     constexpr int STEP = CT * WPS;    // tokens per round of the split's waves
     const int grp = lane >> 4, li = lane & 15;
     const size_t tok_stride = (size_t)H_kv * D;
-    const KV* kbase = kcache + (size_t)kvh * D + li * EPL;
-    const KV* vbase = vcache + (size_t)kvh * D + li * EPL;
+    // d = 128 bf16 rings keep their loads in place (measured 2-5% faster at
+    // ctx 4096-32768); fp32 rings need the register room sinking gives them
+    // and d = 64 bf16 measured 9% slower.
+    constexpr bool OPQ = sizeof(KV) == 2 && D == 128;
+    const KV* kbase = (OPQ ? opaque_global(kcache) : kcache) + (size_t)kvh * D + li * EPL;
+    const KV* vbase = (OPQ ? opaque_global(vcache) : vcache) + (size_t)kvh * D + li * EPL;
 
     // Each wave walks its chunks, keeping the next R - 1 chunks' loads in
     // flight while it computes the current one.  With block size 16 a chunk
@@ -504,7 +705,7 @@ __device__ __forceinline__ void write_partial(float* __restrict__ dst, const flo
 // lengths, so results do not depend on block placement.  Measured at ctx 8192
 // fp32 (four-head workgroups, one per CU): 0.676 of HBM peak against 0.599
 // for the (b, split) grid; bf16 at ctx 32768: 0.684 against 0.625.
-template <int D, int G, typename KV, bool BS16, int R, int NT>
+template <int D, int G, typename KV, bool BS16, int R, int NT, bool KL = false>
 __global__ __launch_bounds__(NT) void decode_attn_balanced_kernel(
     const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
     const int* __restrict__ block_table, const int* __restrict__ context_lens, int B, int H_q,
@@ -578,8 +779,12 @@ __global__ __launch_bounds__(NT) void decode_attn_balanced_kernel(
             const int tok0 = 16 * (max(lo, pre) - pre);
             const int tok1 = min(16 * (min(hi, post) - pre), lb);
             float m[G], l[G], o[G][EPL];
-            split_partial<D, G, KV, 1, BS16, R>(Q, kcache, vcache, block_table + (size_t)bj * nbps, bj, kvh, H_q,
-                                             H_kv, block_size, tok0, tok1, 0, lane, qscale, m, l, o);
+            if constexpr (KL)
+                split_partial_klds<G, NT / 64>(Q, kcache, vcache, block_table + (size_t)bj * nbps, bj, kvh, H_q, H_kv,
+                                                tok0, tok1, lane, qscale, m, l, o);
+            else
+                split_partial<D, G, KV, 1, BS16, R>(Q, kcache, vcache, block_table + (size_t)bj * nbps, bj, kvh, H_q,
+                                                 H_kv, block_size, tok0, tok1, 0, lane, qscale, m, l, o);
             if (grp == 0 && seg < num_splits) {
 #pragma unroll
                 for (int g = 0; g < G; ++g)
@@ -637,8 +842,8 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
     // share a workgroup, so the heads' slices of each block (contiguous in
     // the cache row) are read together; measured 5% faster than one wave per
     // workgroup at ctx 8192.
-    constexpr int HWMAX = wave_heads<D, KV>();
-    constexpr int RW = wave_ring<D, KV>();
+    constexpr int HWMAX = wave_heads<D, KV, G>();
+    constexpr int RW = wave_ring<D, KV, G>();
     constexpr int NTW = 64 * HWMAX;
     int hw = 1;
     if (wave)
@@ -655,8 +860,12 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
     if (wave && a.num_splits >= 2 && a.B <= kBalancedMaxB) {
         // As many workgroups as are resident at once (occupancy x CUs), so the
         // equal ranges all run in one round.
-        auto* kb = bs16 ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW>
-                        : decode_attn_balanced_kernel<D, G, KV, false, RW, NTW>;
+        // fp32 d = 128 with block size 16 lands K in LDS (G = 8 has no
+        // register room for the ring beside its 8 heads' q and o).
+        constexpr bool KL = D == 128 && sizeof(KV) == 4 && G <= 4;
+        auto* kb = (KL && a.block_size == 16) ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW, KL>
+                   : bs16                     ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW>
+                                              : decode_attn_balanced_kernel<D, G, KV, false, RW, NTW>;
         const int gy = a.H_kv / hw;
         const unsigned W = (unsigned)std::max(1, resident_per_cu((const void*)kb, 64 * hw) * num_cus() / gy);
         // chunks the plan covers (S x blocks per split, at least max_context_len)
