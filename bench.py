@@ -15,6 +15,8 @@ inputs.  The same JSON line carries:
                 (GQA, ctx 4096/8192/32768, fp32 and bf16 KV), GB/s of
                 algorithmic bytes against HBM
   e2e_gpt2      GPT-2 Small decode tok/s (BASELINE cfg5), batch 1 and 16
+  sampler       top-k sampling: device selection kernel, one sample_top_k
+                call, the reference's whole-row copy, sampled decode at batch 1
   cpu_baseline  the C oracle (oracle/liborc.so) on a bounded sample of the
                 8192^3 GEMM, on this host's cores
   traffic       HBM bytes per launch of the dominant kernels (rocprofv3
@@ -48,7 +50,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--skip", default="", help="comma list of vendor,gemv,gemm512,attn,cpu,e2e")
+    ap.add_argument("--skip", default="", help="comma list of vendor,gemv,gemm512,attn,cpu,e2e,sampler")
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE passes")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
@@ -335,10 +337,63 @@ def bench_e2e(ie):
     return out
 
 
+def bench_sampler(ie):
+    """Top-k sampling of GPT-2 logits (src/sampler.cu:16-45; k = 40, T = 0.8 as
+    the reference TUI): the device selection kernel alone (rows 1 and 16), one
+    whole sample_top_k call (selection, two k-pair copies, host draw), the
+    201 KB row copy the reference's route starts with, and sampled decode of
+    GPT-2 Small at batch 1 (prompt 128, 256 new tokens)."""
+    import ctypes
+    import numpy as np
+    import torch
+
+    V, k = 50257, 40
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(40)
+    for rows in (1, 16):
+        x = torch.randn((rows, V), device="cuda", generator=g) * 3 - 80
+        vals = torch.empty((rows, k), device="cuda")
+        idx = torch.empty((rows, k), dtype=torch.int32, device="cuda")
+
+        def launch(i, x=x, vals=vals, idx=idx, rows=rows):  # on the capturing stream
+            ie.check("ie_topk", rows, ie._ptr(x), V, k, ie._ptr(vals), ie._ptr(idx), ie._stream())
+
+        out[f"topk_kernel_us_rows{rows}"] = round(graph_time(launch, 20) * 1e3, 2)
+    lib = ie.load()
+    fn = getattr(lib, "_Z12sample_top_kPKfiifj")
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_uint]
+    row = (torch.randn(V, device="cuda", generator=g) * 3 - 80).contiguous()
+    for s in range(20):
+        fn(ctypes.c_void_p(row.data_ptr()), V, k, 0.8, 1000 + s)
+    n = 300
+    t0 = time.perf_counter()
+    for s in range(n):
+        fn(ctypes.c_void_p(row.data_ptr()), V, k, 0.8, 2000 + s)
+    out["sample_top_k_call_us"] = round((time.perf_counter() - t0) / n * 1e6, 1)
+    host = np.empty(V, dtype=np.float32)
+    for _ in range(20):
+        host[:] = row.cpu().numpy()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        host[:] = row.cpu().numpy()
+    out["reference_row_copy_us"] = round((time.perf_counter() - t0) / n * 1e6, 1)
+    eng = ie.Engine(None, seed=1234, max_batch=1)
+    prompt = np.random.default_rng(129).integers(0, 50257, 128).astype(np.int32)
+    eng.generate_one(prompt, 8, temperature=0.8, top_k=k)
+    toks, m = eng.generate_one(prompt, 256, temperature=0.8, top_k=k)
+    eng.close()
+    out["e2e_b1_sampled"] = {"sampling": f"top-k {k}, T 0.8, seeds 42, 43, ...", "decode_tok_s": round(m["tps"], 1),
+                             "tpot_ms": round(m["tpot_ms"], 4), "ttft_ms": round(m["ttft_ms"], 2),
+                             "tokens": len(toks)}
+    log(f"sampler {out}")
+    return out
+
+
 # ------------------------------------------------------------------ HBM traffic
 CALIB_BYTES = 1 << 30
 TRAFFIC_KERNELS = {"gemm": "gemm_i8_256_kernel", "gemv": "gemv_i8_fixed_kernel",
-                   "attn": "decode_attn_split_kernel"}
+                   "attn": "decode_attn_balanced_kernel"}
 
 
 def pmc_child(ie):
@@ -507,6 +562,8 @@ def main():
             res["decode_attn_roofline"]["kernel"] = "decode_attn cfg4 ctx 8192 fp32"
         if "e2e" not in skip:
             res["e2e_gpt2"] = bench_e2e(ie)
+        if "sampler" not in skip:
+            res["sampler"] = bench_sampler(ie)
     if "cpu" not in skip:
         log("cpu baseline")
         res["cpu_baseline"] = cpu_baseline(h["inputs"])

@@ -317,4 +317,14 @@ int ie_argmax(int rows, const float* logits, int n, int* out_idx, ie_stream_t st
     return ie::check_launch("argmax");
 }
 
+int ie_topk(int rows, const float* logits, int n, int k, float* out_vals, int* out_idx, ie_stream_t stream) {
+    if (rows < 0 || n <= 0) return ie::fail(IE_ERR_INVALID, "topk: bad sizes");
+    if (k < 1 || k > n || k > ie::kTopkMax)
+        return ie::fail(IE_ERR_INVALID, "topk: k=%d outside [1, min(n=%d, %d)]", k, n, ie::kTopkMax);
+    if (rows == 0) return IE_OK;
+    if (!logits || !out_vals || !out_idx) return ie::fail(IE_ERR_INVALID, "topk: null pointer");
+    ie::launch_topk(rows, logits, n, k, out_vals, out_idx, (hipStream_t)stream);
+    return ie::check_launch("topk");
+}
+
 }  // extern "C"

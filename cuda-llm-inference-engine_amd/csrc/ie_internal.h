@@ -153,4 +153,9 @@ void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits
 void launch_argmax(int rows, const float* logits, int n, int* out,
                    hipStream_t s);
 
+// ---- top-k sampler (sampler.hip, host/sampler.cpp) ----
+constexpr int kTopkMax = 1024;  // largest k selected on the device
+void launch_topk(int rows, const float* logits, int n, int k, float* out_vals,
+                 int* out_idx, hipStream_t s);
+
 }  // namespace ie

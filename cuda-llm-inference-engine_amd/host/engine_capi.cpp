@@ -121,6 +121,24 @@ int ie_engine_generate(ie_engine* e, int batch, int prompt_len, const int* promp
     });
 }
 
+int ie_engine_generate_one(ie_engine* e, int prompt_len, const int* prompt, int max_new, float temperature,
+                           int top_k, int greedy, int reset_kv, int* out_tokens, int* n_out, ie_metrics* metrics) {
+    if (!e || !prompt || prompt_len <= 0 || max_new < 0)
+        return ie::fail(IE_ERR_INVALID, "ie_engine_generate_one: bad arguments");
+    if (!greedy && !(temperature > 0.0f))
+        return ie::fail(IE_ERR_INVALID, "ie_engine_generate_one: temperature must be > 0 when sampling");
+    return guarded("ie_engine_generate_one", [&] {
+        std::vector<int> p(prompt, prompt + prompt_len), got;
+        InferenceMetrics m;
+        e->eng->generate(p, max_new, temperature, top_k, greedy != 0, [&](int t) { got.push_back(t); }, m,
+                         reset_kv != 0);
+        if (out_tokens)
+            for (int t = 0; t < max_new; ++t) out_tokens[t] = t < (int)got.size() ? got[t] : -1;
+        if (n_out) *n_out = (int)got.size();
+        to_c(m, metrics);
+    });
+}
+
 namespace {
 // Host copies of the logits [batch, V] left by the last step or prefill, and
 // their first-maximum ids.

@@ -266,6 +266,11 @@ struct GPT2Engine::Impl {
 
     int pos = 0;  // host mirror: tokens in every active sequence
     int* host_tokens = nullptr;  // pinned [max_batch]
+    // top-k sampler: device selection [kTopkMax] and its pinned host copy
+    float* topk_vals = nullptr;
+    int* topk_idx = nullptr;
+    float* host_topk_vals = nullptr;
+    int* host_topk_idx = nullptr;
 
     // Prefill scratch [rows, ...], rows = sequences x chunk tokens, grown on
     // first use (the decode step never touches it).
@@ -370,6 +375,10 @@ struct GPT2Engine::Impl {
                     ie::gemv_fused_supported(m, ff, ie::kSrcQuant, IE_EPI_BIAS_RESIDUAL) &&
                     ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, IE_EPI_PLAIN);
         HIPC(hipHostMalloc(&host_tokens, sizeof(int) * B));
+        topk_vals = dev<float>(ie::kTopkMax);
+        topk_idx = dev<int>(ie::kTopkMax);
+        HIPC(hipHostMalloc(&host_topk_vals, sizeof(float) * ie::kTopkMax));
+        HIPC(hipHostMalloc(&host_topk_idx, sizeof(int) * ie::kTopkMax));
         reset();
     }
 
@@ -380,6 +389,8 @@ struct GPT2Engine::Impl {
         for (void* p : pf_allocs) (void)hipFree(p);
         if (pf.host_ids) (void)hipHostFree(pf.host_ids);
         if (host_tokens) (void)hipHostFree(host_tokens);
+        if (host_topk_vals) (void)hipHostFree(host_topk_vals);
+        if (host_topk_idx) (void)hipHostFree(host_topk_idx);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -740,26 +751,36 @@ void GPT2Engine::step(const int* tokens, int batch) {
     impl_->step_tokens(tokens, batch, false);
 }
 
-// src/sampler.cu:16-45: top-k over temperature-scaled softmax, host side.
-static int sample_top_k_host(const std::vector<float>& h, int k, float temperature, std::mt19937& gen) {
-    const int V = (int)h.size();
+// src/sampler.cu:16-45 for sequence 0's logits: the k largest on the device
+// (ie_topk), then the reference's softmax and draw on the host
+// (ie_top_k_draw, srand(seed) / rand()).  k above IE_TOPK_MAX takes the
+// reference's own route, the whole row to the host, with the same order for
+// equal values (lower index first) and the same draw.
+static int sample_top_k_engine(const float* d_logits, int V, int k, float temperature, unsigned seed,
+                               float* d_vals, int* d_idx, float* h_vals, int* h_idx, hipStream_t s) {
     k = std::max(1, std::min(k, V));
+    int token = 0;
+    if (k <= ie::kTopkMax) {
+        if (ie_topk(1, d_logits, V, k, d_vals, d_idx, s) != IE_OK) throw std::runtime_error(ie_last_error());
+        HIPC(hipMemcpyAsync(h_vals, d_vals, sizeof(float) * k, hipMemcpyDeviceToHost, s));
+        HIPC(hipMemcpyAsync(h_idx, d_idx, sizeof(int) * k, hipMemcpyDeviceToHost, s));
+        HIPC(hipStreamSynchronize(s));
+        if (ie_top_k_draw(h_vals, h_idx, k, temperature, seed, &token) != IE_OK)
+            throw std::runtime_error(ie_last_error());
+        return token;
+    }
+    std::vector<float> h(V);
+    HIPC(hipMemcpyAsync(h.data(), d_logits, sizeof(float) * V, hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
     std::vector<int> idx(V);
     std::iota(idx.begin(), idx.end(), 0);
-    std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), [&](int a, int b) { return h[a] > h[b]; });
-    std::vector<float> p(k);
-    float sum = 0.0f;
-    for (int i = 0; i < k; ++i) {
-        p[i] = std::exp((h[idx[i]] - h[idx[0]]) / temperature);
-        sum += p[i];
-    }
-    const float r = std::uniform_real_distribution<float>(0.0f, 1.0f)(gen);
-    float cum = 0.0f;
-    for (int i = 0; i < k; ++i) {
-        cum += p[i] / sum;
-        if (r < cum) return idx[i];
-    }
-    return idx[k - 1];
+    std::partial_sort(idx.begin(), idx.begin() + k, idx.end(),
+                      [&](int a, int b) { return h[a] > h[b] || (h[a] == h[b] && a < b); });
+    std::vector<float> vals(k);
+    for (int i = 0; i < k; ++i) vals[i] = h[idx[i]];
+    if (ie_top_k_draw(vals.data(), idx.data(), k, temperature, seed, &token) != IE_OK)
+        throw std::runtime_error(ie_last_error());
+    return token;
 }
 
 void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tokens, float temperature,
@@ -771,13 +792,16 @@ void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tok
     metrics.generating = true;
     if (prompt_tokens.empty()) throw std::runtime_error("empty prompt");
     if (reset_kv) I.reset();
-    std::mt19937 gen(42u);
-    std::vector<float> hl;
+    // Seeds as the reference's loop passes them: 42 for the token after the
+    // prompt, then 43, 44, ... (src/gpt2_engine.cu:707, 713, 747).
+    unsigned sample_seed = 42u;
+    bool first_pick = true;
     auto pick = [&]() -> int {
         if (greedy) return I.host_tokens[0];
-        hl.resize(I.cfg.vocab_size);
-        HIPC(hipMemcpy(hl.data(), I.logits, sizeof(float) * hl.size(), hipMemcpyDeviceToHost));
-        return sample_top_k_host(hl, top_k, temperature, gen);
+        const unsigned seed = first_pick ? 42u : ++sample_seed;
+        first_pick = false;
+        return sample_top_k_engine(I.logits, I.cfg.vocab_size, top_k, temperature, seed, I.topk_vals, I.topk_idx,
+                                   I.host_topk_vals, I.host_topk_idx, I.stream);
     };
 
     const auto t_total = Clock::now();

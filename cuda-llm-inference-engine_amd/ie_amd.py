@@ -44,6 +44,8 @@ SIGNATURES = {
     "ie_embedding_batch": (_I, [_I, _P, _P, _I, _P, _P, _P, _P]),
     "ie_vocab_proj": (_I, [_I, _P, _P, _P, _I, _I, _P]),
     "ie_argmax": (_I, [_I, _P, _I, _P, _P]),
+    "ie_topk": (_I, [_I, _P, _I, _I, _P, _P, _P]),
+    "ie_top_k_draw": (_I, [_P, _P, _I, _F, ctypes.c_uint, _P]),
 }
 
 # include/ie_engine.h
@@ -54,6 +56,7 @@ ENGINE_SIGNATURES = {
     "ie_engine_write_random_model": (_I, [ctypes.c_char_p, _I, _I, _I, _I, _I, _I, ctypes.c_ulonglong]),
     "ie_engine_reset": (_I, [_P]),
     "ie_engine_generate": (_I, [_P, _I, _I, _P, _I, _I, _P, _P]),
+    "ie_engine_generate_one": (_I, [_P, _I, _P, _I, _F, _I, _I, _I, _P, _P, _P]),
     "ie_engine_step": (_I, [_P, _I, _P, _P, _P]),
     "ie_engine_prefill": (_I, [_P, _I, _I, _P, _P, _P]),
     "ie_engine_session_tokens": (_I, [_P]),
@@ -269,6 +272,30 @@ def argmax(logits, out=None, stream=None):
     return out
 
 
+def topk(logits, k, stream=None):
+    """(values [rows, k] fp32, indices [rows, k] int32) of the k largest per row,
+    by value descending, equal values by index ascending."""
+    import torch
+
+    rows, n = logits.shape
+    vals = torch.empty((rows, k), dtype=torch.float32, device=logits.device)
+    idx = torch.empty((rows, k), dtype=torch.int32, device=logits.device)
+    check("ie_topk", rows, _ptr(logits), n, k, _ptr(vals), _ptr(idx), _stream(stream))
+    return vals, idx
+
+
+def top_k_draw(vals, idx, temperature, seed):
+    """Host draw of sample_top_k over sorted (value, index) pairs (numpy)."""
+    import numpy as np
+
+    v = np.ascontiguousarray(vals, dtype=np.float32)
+    i = np.ascontiguousarray(idx, dtype=np.int32)
+    tok = ctypes.c_int(-1)
+    check("ie_top_k_draw", v.ctypes.data, i.ctypes.data, len(v), ctypes.c_float(temperature),
+          ctypes.c_uint(seed), ctypes.addressof(tok))
+    return tok.value
+
+
 # ---------------------------------------------------------------- engine
 GPT2_SMALL = dict(n_layers=12, n_heads=12, d_model=768, d_ff=3072, vocab_size=50257, max_seq_len=1024)
 
@@ -341,6 +368,19 @@ class Engine:
         check("ie_engine_generate", self.h, B, P, p.ctypes.data_as(ctypes.c_void_p), max_new, int(ignore_eos),
               out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(m))
         return out, m.as_dict()
+
+    def generate_one(self, prompt, max_new, temperature=0.8, top_k=40, greedy=False, reset=True):
+        """GPT2Engine::generate for one prompt -> (generated ids, metrics dict)."""
+        import numpy as np
+
+        p = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
+        out = np.full(max_new, -1, dtype=np.int32)
+        n = ctypes.c_int(0)
+        m = Metrics()
+        check("ie_engine_generate_one", self.h, len(p), p.ctypes.data_as(ctypes.c_void_p), max_new,
+              ctypes.c_float(temperature), top_k, int(greedy), int(reset), out.ctypes.data_as(ctypes.c_void_p),
+              ctypes.byref(n), ctypes.byref(m))
+        return out[: n.value].tolist(), m.as_dict()
 
     def session_tokens(self):
         return load().ie_engine_session_tokens(self.h)

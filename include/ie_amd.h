@@ -25,6 +25,9 @@
  *   ie_embedding              run_embedding  kernels/layernorm/15_embed.cu:24-30
  *   ie_vocab_proj             run_vocab_proj src/gpt2_engine.cu:391-410
  *   ie_argmax                 sample_argmax  src/sampler.cu:10-14 (device-side)
+ *   ie_topk                   sample_top_k's partial_sort, src/sampler.cu:20-26
+ *                             (device-side; only k pairs reach the host)
+ *   ie_top_k_draw             sample_top_k's softmax and draw, src/sampler.cu:28-44
  * The reference's own C++ signatures are kept, unchanged, in ie_compat.h.
  */
 #ifndef IE_AMD_H
@@ -171,6 +174,24 @@ int ie_vocab_proj(int rows, const float* hidden, const float* wte,
 /* out_idx[r] = first index of the maximum of logits[r, 0:n]. */
 int ie_argmax(int rows, const float* logits, int n, int* out_idx,
               ie_stream_t stream);
+
+/* Largest k selectable by ie_topk. */
+#define IE_TOPK_MAX 1024
+/* The k largest of logits[r, 0:n] for each row r, 1 <= k <= min(n,
+ * IE_TOPK_MAX): out_vals[r, 0:k] by value descending, equal values by index
+ * ascending, out_idx[r, 0:k] their indices (device pointers).  NaN logits
+ * are not supported. */
+int ie_topk(int rows, const float* logits, int n, int k, float* out_vals,
+            int* out_idx, ie_stream_t stream);
+/* Host side of sample_top_k: from k >= 1 sorted (value, index) pairs, such
+ * as ie_topk's (host memory), p_i = expf((v_i - v_0) / temperature) normalised,
+ * and the first i whose running sum exceeds r = rand() / RAND_MAX, where the
+ * generator is reseeded with srand(seed) whenever seed differs from the
+ * previous call's (the reference's rule).  The library keeps that generator
+ * state privately (glibc's rand() algorithm), so the process-wide rand() is
+ * untouched.  *token = the chosen index. */
+int ie_top_k_draw(const float* vals, const int* idx, int k, float temperature,
+                  unsigned int seed, int* token);
 
 #ifdef __cplusplus
 }

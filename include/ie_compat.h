@@ -8,6 +8,7 @@
  *   kernels/flash_attention/10_flash_attn_v2.cuh   run_flash_attn_v2
  *   kernels/layernorm/15_layernorm_residual.cuh    run_layernorm
  *   kernels/layernorm/15_embed.cuh                 run_embedding
+ *   include/sampler.cuh                            sample_argmax, sample_top_k
  *
  * As in the reference: void return, caller-owned device pointers, the null
  * stream, asynchronous.  Unlike the reference, invalid arguments never reach a
@@ -65,5 +66,16 @@ void run_layernorm(int rows, int cols, const float* x, const float* gamma,
 
 void run_embedding(const int* token_ids, int seq_len, int start_pos,
                    int d_model, const float* wte, const float* wpe, float* out);
+
+/* Samplers over device logits [vocab_size] (src/sampler.cu).  The argmax and
+ * the top-k selection run on the device, so 4 bytes (argmax) or k value/index
+ * pairs (top-k) come back instead of the whole row; k is clamped to
+ * vocab_size as in the reference and must then be <= IE_TOPK_MAX.  The draw
+ * follows the reference's float arithmetic and its srand(seed) / rand() rule
+ * with a generator private to the library (see ie_top_k_draw).  Two small
+ * device buffers are allocated on the first call and kept.  -1 on error. */
+int sample_argmax(const float* d_logits, int vocab_size);
+int sample_top_k(const float* d_logits, int vocab_size, int k,
+                 float temperature, unsigned int seed);
 
 #endif

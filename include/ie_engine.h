@@ -43,6 +43,14 @@ int ie_engine_reset(ie_engine* e);
  * out_tokens [batch, max_new] receives the ids, -1 past a sequence's end. */
 int ie_engine_generate(ie_engine* e, int batch, int prompt_len, const int* prompts, int max_new,
                        int ignore_eos, int* out_tokens, ie_metrics* metrics);
+/* GPT2Engine::generate for one prompt (src/gpt2_engine.cu:628-770):
+ * greedy != 0 takes the argmax, else top-k sampling at `temperature` with
+ * the reference's seeds (42, then 43, 44, ...).  Stops at <|endoftext|>
+ * (50256) as the reference.  out_tokens [max_new] receives the ids, -1 past
+ * the end; *n_out the count.  reset_kv != 0 starts a fresh session. */
+int ie_engine_generate_one(ie_engine* e, int prompt_len, const int* prompt, int max_new,
+                           float temperature, int top_k, int greedy, int reset_kv,
+                           int* out_tokens, int* n_out, ie_metrics* metrics);
 /* One decode step at the current position; optional host copies of the
  * logits [batch, vocab] and of the argmax ids [batch]. */
 int ie_engine_step(ie_engine* e, int batch, const int* tokens, float* logits_host,

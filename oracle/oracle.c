@@ -501,3 +501,66 @@ int orc_argmax(const float* logits, int n) {
         if (logits[i] > logits[best]) best = i;
     return best;
 }
+
+/* ------------------------------------------------------------------------
+ * Top-k sampler, src/sampler.cu:16-45.
+ *   k = min(k, V)                                                  (:21)
+ *   indices ordered by logit descending, first k kept              (:22-25)
+ *     (std::partial_sort leaves equal logits in unspecified order; here the
+ *     lower index comes first, the order a stable sort gives)
+ *   probs[i] = expf((h[idx[i]] - h[idx[0]]) / temperature), summed (:27-32)
+ *   probs[i] /= sum                                                (:33)
+ *   r = (float)rand() / RAND_MAX                                   (:35-37)
+ *   first i with r < probs[0] + ... + probs[i], else idx[k-1]      (:38-44)
+ * ---------------------------------------------------------------------- */
+static const float* g_topk_row;
+
+static int topk_cmp(const void* pa, const void* pb) {
+    const int a = *(const int*)pa, b = *(const int*)pb;
+    const float x = g_topk_row[a], y = g_topk_row[b];
+    if (x > y) return -1;
+    if (y > x) return 1;
+    return a < b ? -1 : (a > b);
+}
+
+int orc_topk(int rows, int n, int k, const float* logits, float* vals, int* idx) {
+    if (rows < 0 || n <= 0 || k < 1 || k > n) return 1;
+    int* order = (int*)malloc(sizeof(int) * (size_t)n);
+    if (!order) return 2;
+    for (int r = 0; r < rows; ++r) {
+        g_topk_row = logits + (size_t)r * n;
+        for (int i = 0; i < n; ++i) order[i] = i;
+        qsort(order, (size_t)n, sizeof(int), topk_cmp);
+        for (int i = 0; i < k; ++i) {
+            vals[(size_t)r * k + i] = g_topk_row[order[i]];
+            idx[(size_t)r * k + i] = order[i];
+        }
+    }
+    free(order);
+    return 0;
+}
+
+float orc_rand_unit(void* rng) { return (float)orc_rng_next(rng) / (float)RAND_MAX; }
+
+int orc_top_k_draw(const float* vals, const int* idx, int k, float temperature, float r) {
+    float* probs = (float*)malloc(sizeof(float) * (size_t)k);
+    if (!probs) return -1;
+    const float max_val = vals[0];
+    float sum = 0.0f;
+    for (int i = 0; i < k; ++i) {
+        probs[i] = expf((vals[i] - max_val) / temperature);
+        sum += probs[i];
+    }
+    for (int i = 0; i < k; ++i) probs[i] /= sum;
+    float cum = 0.0f;
+    int out = idx[k - 1];
+    for (int i = 0; i < k; ++i) {
+        cum += probs[i];
+        if (r < cum) {
+            out = idx[i];
+            break;
+        }
+    }
+    free(probs);
+    return out;
+}

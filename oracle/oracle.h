@@ -27,6 +27,14 @@
  *   orc_layernorm             torch layer_norm in fp64
  *   orc_embedding, orc_vocab_proj, orc_argmax
  *                             numpy gather / matmul / argmax
+ *   orc_topk                  Python sorted() by (-value, index) brute force,
+ *                             numpy argsort, k = n is a permutation
+ *   orc_top_k_draw            k = 1 and a cold temperature pick idx[0]; r just
+ *                             below / above a hand-computed cumulative bound;
+ *                             pick frequencies over 20000 seeds against the
+ *                             softmax probabilities (chi-square)
+ *   Ties in orc_topk: the reference's partial_sort leaves their order
+ *   unspecified, so that order is parity unpinned against the reference.
  */
 #ifndef IE_ORACLE_H
 #define IE_ORACLE_H
@@ -110,6 +118,14 @@ void orc_vocab_proj(const float* hidden, const float* wte, float* logits,
                     int d, int V);
 /* src/sampler.cu:10-14: first index of the maximum */
 int orc_argmax(const float* logits, int n);
+
+/* ---- top-k sampler: src/sampler.cu:16-45 ----
+ * orc_topk: the k largest of each row, value descending, equal values by
+ * index ascending.  orc_rand_unit: (float)rand() / RAND_MAX (:37).
+ * orc_top_k_draw: the index drawn at threshold r from sorted pairs. */
+int orc_topk(int rows, int n, int k, const float* logits, float* vals, int* idx);
+float orc_rand_unit(void* rng);
+int orc_top_k_draw(const float* vals, const int* idx, int k, float temperature, float r);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,9 @@ SIGNATURES = {
     "orc_embedding": (None, [_P, _I, _I, _I, _P, _P, _P]),
     "orc_vocab_proj": (None, [_P, _P, _P, _I, _I]),
     "orc_argmax": (_I, [_P, _I]),
+    "orc_topk": (_I, [_I, _I, _I, _P, _P, _P]),
+    "orc_rand_unit": (ctypes.c_float, [_P]),
+    "orc_top_k_draw": (_I, [_P, _P, _I, ctypes.c_float, ctypes.c_float]),
 }
 
 _lib = None
@@ -213,3 +216,38 @@ def vocab_proj(h, wte):
 def argmax(logits) -> int:
     logits = _c(logits, np.float32)
     return load().orc_argmax(_p(logits), logits.shape[0])
+
+
+def topk(logits, k):
+    """logits [rows, n] -> (values [rows, k], indices [rows, k]); src/sampler.cu:20-26."""
+    logits = _c(np.atleast_2d(logits), np.float32)
+    rows, n = logits.shape
+    vals = np.empty((rows, k), dtype=np.float32)
+    idx = np.empty((rows, k), dtype=np.int32)
+    if load().orc_topk(rows, n, k, _p(logits), _p(vals), _p(idx)) != 0:
+        raise ValueError("orc_topk: bad arguments")
+    return vals, idx
+
+
+def rand_unit(seed: int, skip: int = 0) -> float:
+    """(float)rand() / RAND_MAX for the (skip+1)-th rand() after srand(seed)."""
+    g = GlibcRand(seed)
+    for _ in range(skip):
+        g.next()
+    return load().orc_rand_unit(g._h)
+
+
+def top_k_draw(vals, idx, temperature, r) -> int:
+    """The index drawn at threshold r from sorted pairs; src/sampler.cu:27-44."""
+    v = _c(vals, np.float32)
+    i = _c(idx, np.int32)
+    return load().orc_top_k_draw(_p(v), _p(i), len(v), ctypes.c_float(temperature), ctypes.c_float(r))
+
+
+def sample_top_k(logits, k, temperature, seed, skip=0) -> int:
+    """sample_top_k of one row when srand(seed) was just called (skip = rand()
+    calls since), src/sampler.cu:16-45."""
+    logits = np.asarray(logits, dtype=np.float32).reshape(-1)
+    k = min(k, logits.shape[0])
+    v, i = topk(logits, k)
+    return top_k_draw(v[0], i[0], temperature, rand_unit(seed, skip))

@@ -16,7 +16,7 @@ COMPAT = os.path.join(ROOT, "include", "ie_compat.h")
 LIB = os.path.join(PKG, "libie_amd.so")
 
 
-SIGS_EXPECTED = 18  # entry points declared in include/ie_amd.h
+SIGS_EXPECTED = 20  # entry points declared in include/ie_amd.h
 
 
 def declared_c_functions(path=HDR):
@@ -26,7 +26,7 @@ def declared_c_functions(path=HDR):
 
 def declared_cpp_functions():
     text = open(COMPAT).read()
-    return sorted(set(re.findall(r"^\s*void\s+(run_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:void|int)\s+(run_\w+|sample_\w+)\s*\(", text, re.M)))
 
 
 def exported():
@@ -44,7 +44,7 @@ def test_library_loads_and_exports_all(ie):
     # the ctypes tables cover exactly the headers
     assert sorted(ie.SIGNATURES) == names
     eng = declared_c_functions(ENGINE_HDR)
-    assert len(eng) == 10 and sorted(ie.ENGINE_SIGNATURES) == eng
+    assert len(eng) == 11 and sorted(ie.ENGINE_SIGNATURES) == eng
     for n in eng:
         assert hasattr(lib, n), n
     syms = exported()
