@@ -7,19 +7,21 @@
 // softmax over the k values and the rand() threshold) stays on the host,
 // where it is the same float arithmetic as the reference's.
 //
-// One 1024-thread workgroup per row:
-//   1. radix select of the k-th largest order key, 8 bits per pass from the
-//      top.  The histogram lives in LDS; logits cluster in a few exponent
-//      bins, so each wave instruction adds its leading lane's bin with one
-//      atomic and only the other lanes' bins lane by lane;
-//   2. gather: every key above the threshold, plus the lowest-index keys equal
-//      to it (ranked in index order only when some equal keys are left out),
-//      k entries in LDS;
-//   3. bitonic sort of the k entries (padded to a power of two) in LDS.
-// Rows of up to 64 x 1024 logits (GPT-2's 50257 among them) are read once
-// into registers, 64 keys per thread, and every pass runs from there; longer
-// rows are streamed from memory (L2 after the first pass) with 8 loads in
-// flight per thread.
+// One 1024-thread workgroup per row.  Rows of up to 65533 logits (GPT-2's
+// 50257 among them) are read once, as 16-byte chunks, into registers (64 keys
+// per thread):
+//   1. a lower bound M of the k-th largest key: the k-th largest of the 1024
+//      per-thread maxima (a radix select over one key per thread);
+//   2. the keys >= M (typically a few more than k) gathered into LDS;
+//   3. each gathered key ranked by counting those before it (larger key, or
+//      equal key and lower index), and the first k written.
+// Longer rows, and rows where more than 2048 keys reach M (many equal
+// values, or k near 1024), are streamed from memory (L2 after the first
+// pass) through an exact radix select of the k-th largest key, 8 bits per
+// pass (the histogram in LDS; each wave instruction adds its leading lane's
+// bin with one atomic, the other lanes' bins lane by lane), a gather of the
+// keys above it plus the lowest-index keys equal to it (ranked in index order
+// only when some equal keys are left out), and a bitonic sort of those k.
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -34,6 +36,7 @@ constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / 64;
 constexpr int kTopkUnroll = 8;
 constexpr int kTopkRegPer = 64;  // keys per thread in the register-resident kernel
+constexpr int kTopkCand = 2048;  // candidates (keys >= the lower bound) sorted directly
 
 // Unsigned key with the order of the floats; -0.0 is keyed as +0.0 so that
 // values the reference compares equal are equal here.
@@ -50,11 +53,9 @@ __device__ __forceinline__ float key_value(uint32_t k) {
 struct TopkShared {
     uint32_t hist[256];
     uint32_t prefix, remaining, eqcount, gt, eq;
-    uint32_t scan[kTopkThreads];  // tie ranks: counts per (column, wave), then their exclusive prefix
-    uint64_t emask[kTopkThreads];  // tie ranks: lanes holding a key equal to the threshold, per (column, wave)
     uint32_t wave_tot[kTopkWaves];
-    uint32_t ckey[kTopkMax];
-    int cidx[kTopkMax];
+    uint32_t ckey[kTopkCand];
+    int cidx[kTopkCand];
 };
 
 // Adds one key per lane (where `match`) to bin `digit`: the leading lane's
@@ -106,23 +107,6 @@ __device__ __forceinline__ void put(TopkShared& sh, uint32_t slot, uint32_t key,
     sh.cidx[slot] = i;
 }
 
-// Exclusive prefix of sh.scan[0 .. 1024) in place (all threads).
-__device__ __forceinline__ void block_exclusive_scan(TopkShared& sh, int lane, int wid) {
-    const uint32_t v = sh.scan[threadIdx.x];
-    uint32_t incl = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t t = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += t;
-    }
-    if (lane == 63) sh.wave_tot[wid] = incl;
-    __syncthreads();
-    uint32_t base = 0;
-    for (int w = 0; w < wid; ++w) base += sh.wave_tot[w];
-    sh.scan[threadIdx.x] = base + incl - v;
-    __syncthreads();
-}
-
 // Radix select of the k-th largest key, 8 bits per pass from the top:
 // add(hmask, prefix, shift) puts every candidate key whose bits under hmask
 // equal prefix into bin (key >> shift) & 255.  Returns the key; `remaining`
@@ -150,12 +134,12 @@ __device__ __forceinline__ uint32_t radix_kth(TopkShared& sh, uint32_t k, Add&& 
     return prefix;
 }
 
-// Bitonic sort of the k gathered entries (larger key first, then lower
-// index) and the output row.
-__device__ __forceinline__ void sort_and_write(TopkShared& sh, int k, float* out_vals, int* out_idx) {
+// Bitonic sort of the `count` gathered entries (larger key first, then
+// lower index); the first k are the output row.
+__device__ __forceinline__ void sort_and_write(TopkShared& sh, int count, int k, float* out_vals, int* out_idx) {
     int KP = 1;
-    while (KP < k) KP <<= 1;
-    for (int t = k + threadIdx.x; t < KP; t += kTopkThreads) put(sh, t, 0u, INT_MAX);
+    while (KP < count) KP <<= 1;
+    for (int t = count + threadIdx.x; t < KP; t += kTopkThreads) put(sh, t, 0u, INT_MAX);
     __syncthreads();
     for (int size = 2; size <= KP; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -179,93 +163,10 @@ __device__ __forceinline__ void sort_and_write(TopkShared& sh, int k, float* out
     }
 }
 
-// Rows of n <= 64 x 1024: thread t holds keys of indices t + 1024 j; key 0
-// (the bit pattern of a NaN, which rows do not hold) marks indices past n.
-__global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(const float* __restrict__ logits, int n, int k,
-                                                                float* __restrict__ out_vals,
-                                                                int* __restrict__ out_idx) {
-    __shared__ TopkShared sh;
-    const float* x = logits + (size_t)blockIdx.x * n;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    uint32_t key[kTopkRegPer];
-#pragma unroll
-    for (int j = 0; j < kTopkRegPer; ++j) {
-        const int i = (int)threadIdx.x + j * kTopkThreads;
-        key[j] = i < n ? order_key(x[i]) : 0u;
-    }
-    auto valid = [&](int j) { return key[j] != 0u; };
-
-    // Lower bound M: the k-th largest of the 1024 per-thread maxima (k <=
-    // 1024).  Those k maxima are k keys >= M, so every key of the top k is
-    // >= M, and only keys >= M (typically a few more than k) reach the
-    // histogram below: GPT-2's logits otherwise spread over some 60 bins in
-    // the second pass and nearly every key costs an LDS atomic.
-    uint32_t tmax = 0;
-#pragma unroll
-    for (int j = 0; j < kTopkRegPer; ++j) tmax = max(tmax, key[j]);
-    uint32_t remaining, eqcount;
-    const uint32_t M = radix_kth(
-        sh, (uint32_t)k,
-        [&](uint32_t hmask, uint32_t prefix, int shift) {
-            hist_add(sh.hist, (tmax & hmask) == prefix, (tmax >> shift) & 255u, lane);
-        },
-        lane, wid, remaining, eqcount);
-    // (every loop over key[] is fully unrolled: an early exit would leave the
-    // array indexed at run time, i.e. in scratch memory)
-    const uint32_t prefix = radix_kth(
-        sh, (uint32_t)k,
-        [&](uint32_t hmask, uint32_t prefix, int shift) {
-#pragma unroll
-            for (int j = 0; j < kTopkRegPer; ++j)
-                hist_add(sh.hist, valid(j) && key[j] >= M && (key[j] & hmask) == prefix, (key[j] >> shift) & 255u,
-                         lane);
-        },
-        lane, wid, remaining, eqcount);
-    const uint32_t T = prefix, kgt = (uint32_t)k - remaining;
-
-    if (threadIdx.x == 0) sh.gt = sh.eq = 0;
-    if (eqcount == remaining) {  // every key equal to T is taken
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < kTopkRegPer; ++j)
-            if (valid(j) && key[j] >= T)
-                put(sh, key[j] > T ? atomicAdd(&sh.gt, 1u) : kgt + atomicAdd(&sh.eq, 1u), key[j], threadIdx.x + j * kTopkThreads);
-    } else {
-        // rank of each equal key in index order: index t + 1024 j orders by
-        // column j, then wave, then lane
-        const uint64_t below = (1ull << lane) - 1;
-        sh.scan[threadIdx.x] = 0;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < kTopkRegPer; ++j) {
-            const uint64_t m = __ballot(valid(j) && key[j] == T);
-            if (lane == 0) {
-                sh.scan[j * kTopkWaves + wid] = (uint32_t)__popcll(m);
-                sh.emask[j * kTopkWaves + wid] = m;  // kept in LDS, not in 64 scalar register pairs
-            }
-        }
-        __syncthreads();
-        block_exclusive_scan(sh, lane, wid);
-#pragma unroll
-        for (int j = 0; j < kTopkRegPer; ++j) {
-            const bool eq = valid(j) && key[j] == T;
-            const uint64_t m = sh.emask[j * kTopkWaves + wid];
-            const uint32_t r = sh.scan[j * kTopkWaves + wid] + (uint32_t)__popcll(m & below);
-            if (valid(j) && key[j] > T) put(sh, atomicAdd(&sh.gt, 1u), key[j], threadIdx.x + j * kTopkThreads);
-            if (eq && r < remaining) put(sh, kgt + r, key[j], threadIdx.x + j * kTopkThreads);
-        }
-    }
-    __syncthreads();
-    sort_and_write(sh, k, out_vals, out_idx);
-}
-
-// Longer rows, streamed: every pass re-reads the row (L2 after the first).
-__global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(const float* __restrict__ logits, int n, int k,
-                                                                   float* __restrict__ out_vals,
-                                                                   int* __restrict__ out_idx) {
-    __shared__ TopkShared sh;
-    const float* x = logits + (size_t)blockIdx.x * n;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+// Streams one row (every pass re-reads it: L2 after the first).
+__device__ __forceinline__ void topk_stream_row(TopkShared& sh, const float* __restrict__ x, int n, int k,
+                                                float* __restrict__ out_vals, int* __restrict__ out_idx, int lane,
+                                                int wid) {
     // visits every index in rounds of kTopkUnroll coalesced loads per thread
     auto for_each = [&](auto&& f) {
         for (int base = threadIdx.x; base < n; base += kTopkThreads * kTopkUnroll) {
@@ -273,7 +174,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(const float* 
 #pragma unroll
             for (int u = 0; u < kTopkUnroll; ++u) {
                 const int i = base + u * kTopkThreads;
-                v[u] = i < n ? x[i] : 0.0f;
+                v[u] = x[min(i, n - 1)];
             }
 #pragma unroll
             for (int u = 0; u < kTopkUnroll; ++u) f(base + u * kTopkThreads, order_key(v[u]));
@@ -323,14 +224,110 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(const float* 
         }
     }
     __syncthreads();
-    sort_and_write(sh, k, out_vals, out_idx);
+    sort_and_write(sh, k, k, out_vals, out_idx);
+}
+
+// Rows whose 16-byte chunks number at most 16 x 1024 (n + 3 <= 65536): the
+// row is read once as 16-byte chunks from its 16-byte-aligned base, thread t
+// holding chunks t + 1024 q (q < 16), i.e. indices 4 (t + 1024 q) + c - s
+// where s = the row start's float offset within its chunk.  Key 0 (the bit
+// pattern of a NaN, which rows do not hold) marks slots outside the row.
+__global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(const float* __restrict__ logits, int n, int k,
+                                                                float* __restrict__ out_vals,
+                                                                int* __restrict__ out_idx) {
+    __shared__ TopkShared sh;
+    const float* x = logits + (size_t)blockIdx.x * n;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int s = (int)(((uintptr_t)x & 15u) >> 2);
+    const float4* x4 = reinterpret_cast<const float4*>(x - s);
+    // chunks wholly inside the row: [cf, cl]; the (at most two) others that
+    // touch it are read element by element by the one lane that holds each
+    const int cf = s == 0 ? 0 : 1, cl = (n + s) / 4 - 1;
+    uint32_t key[kTopkRegPer];
+#pragma unroll
+    for (int q = 0; q < kTopkRegPer / 4; ++q) {
+        const int c = (int)threadIdx.x + q * kTopkThreads, e0 = 4 * c - s;
+        // branch-free for whole chunks, so all 16 loads are in flight together
+        float4 v = cf <= cl ? x4[min(max(c, cf), cl)] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool whole = c >= cf && c <= cl;
+        if (!whole && e0 < n && e0 + 3 >= 0) {
+            v.x = e0 >= 0 && e0 < n ? x[e0] : 0.f;
+            v.y = e0 + 1 >= 0 && e0 + 1 < n ? x[e0 + 1] : 0.f;
+            v.z = e0 + 2 >= 0 && e0 + 2 < n ? x[e0 + 2] : 0.f;
+            v.w = e0 + 3 < n ? x[e0 + 3] : 0.f;
+        }
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) key[4 * q + u] = e0 + u >= 0 && e0 + u < n ? order_key(e[u]) : 0u;
+    }
+    // index of key[j]: one base per thread plus a constant per slot (written
+    // this way the compiler does not keep 64 precomputed indices live)
+    const int ibase = 4 * (int)threadIdx.x - s;
+    auto index = [&](int j) { return ibase + (j >> 2) * (4 * kTopkThreads) + (j & 3); };
+
+    // Lower bound M: the k-th largest of the 1024 per-thread maxima (k <=
+    // 1024).  Those k maxima are k keys >= M, so every key of the top k is
+    // >= M.  The keys >= M (typically a few more than k) are gathered into
+    // LDS and ranked there; only when more than kTopkCand keys reach M (many
+    // ties, or k near 1024) is the row streamed through the radix select.
+    // (every loop over key[] is fully unrolled: an early exit would leave the
+    // array indexed at run time, i.e. in scratch memory)
+    uint32_t tmax = 0;
+#pragma unroll
+    for (int j = 0; j < kTopkRegPer; ++j) tmax = max(tmax, key[j]);
+    uint32_t remaining, eqcount;
+    const uint32_t M = radix_kth(
+        sh, (uint32_t)k,
+        [&](uint32_t hmask, uint32_t prefix, int shift) {
+            hist_add(sh.hist, (tmax & hmask) == prefix, (tmax >> shift) & 255u, lane);
+        },
+        lane, wid, remaining, eqcount);
+    if (threadIdx.x == 0) sh.gt = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kTopkRegPer; ++j)
+        if (key[j] != 0u && key[j] >= M) {
+            const uint32_t slot = atomicAdd(&sh.gt, 1u);
+            if (slot < (uint32_t)kTopkCand) put(sh, slot, key[j], index(j));
+        }
+    __syncthreads();
+    const uint32_t cnt = sh.gt;
+    if (cnt > (uint32_t)kTopkCand) {  // uniform
+        __syncthreads();  // all have read the count before the stream resets it
+        topk_stream_row(sh, x, n, k, out_vals, out_idx, lane, wid);
+        return;
+    }
+    // rank sort: a candidate's place is the number of candidates before it
+    // (larger key, or equal key and lower index); places are distinct
+    for (int t = threadIdx.x; t < (int)cnt; t += kTopkThreads) {
+        const uint32_t kt = sh.ckey[t];
+        const int it = sh.cidx[t];
+        int rank = 0;
+        for (int u = 0; u < (int)cnt; ++u) {
+            const uint32_t ku = sh.ckey[u];
+            rank += ku > kt || (ku == kt && sh.cidx[u] < it);
+        }
+        if (rank < k) {
+            out_vals[(size_t)blockIdx.x * k + rank] = key_value(kt);
+            out_idx[(size_t)blockIdx.x * k + rank] = it;
+        }
+    }
+}
+
+// Longer rows.
+__global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(const float* __restrict__ logits, int n, int k,
+                                                                   float* __restrict__ out_vals,
+                                                                   int* __restrict__ out_idx) {
+    __shared__ TopkShared sh;
+    topk_stream_row(sh, logits + (size_t)blockIdx.x * n, n, k, out_vals, out_idx, threadIdx.x & 63,
+                    threadIdx.x >> 6);
 }
 
 }  // namespace
 
 void launch_topk(int rows, const float* logits, int n, int k, float* out_vals, int* out_idx, hipStream_t s) {
     if (rows == 0) return;
-    if (n <= kTopkRegPer * kTopkThreads)
+    if (n + 3 <= kTopkRegPer * kTopkThreads)
         topk_reg_kernel<<<rows, kTopkThreads, 0, s>>>(logits, n, k, out_vals, out_idx);
     else
         topk_stream_kernel<<<rows, kTopkThreads, 0, s>>>(logits, n, k, out_vals, out_idx);

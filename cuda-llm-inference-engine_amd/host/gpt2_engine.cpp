@@ -266,11 +266,10 @@ struct GPT2Engine::Impl {
 
     int pos = 0;  // host mirror: tokens in every active sequence
     int* host_tokens = nullptr;  // pinned [max_batch]
-    // top-k sampler: device selection [kTopkMax] and its pinned host copy
-    float* topk_vals = nullptr;
-    int* topk_idx = nullptr;
-    float* host_topk_vals = nullptr;
-    int* host_topk_idx = nullptr;
+    // top-k sampler: k values then k indices in one device buffer
+    // [2 kTopkMax words] and its pinned host copy (one transfer per token)
+    float* topk_buf = nullptr;
+    float* host_topk_buf = nullptr;
 
     // Prefill scratch [rows, ...], rows = sequences x chunk tokens, grown on
     // first use (the decode step never touches it).
@@ -375,10 +374,8 @@ struct GPT2Engine::Impl {
                     ie::gemv_fused_supported(m, ff, ie::kSrcQuant, IE_EPI_BIAS_RESIDUAL) &&
                     ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, IE_EPI_PLAIN);
         HIPC(hipHostMalloc(&host_tokens, sizeof(int) * B));
-        topk_vals = dev<float>(ie::kTopkMax);
-        topk_idx = dev<int>(ie::kTopkMax);
-        HIPC(hipHostMalloc(&host_topk_vals, sizeof(float) * ie::kTopkMax));
-        HIPC(hipHostMalloc(&host_topk_idx, sizeof(int) * ie::kTopkMax));
+        topk_buf = dev<float>(2 * ie::kTopkMax);
+        HIPC(hipHostMalloc(&host_topk_buf, sizeof(float) * 2 * ie::kTopkMax));
         reset();
     }
 
@@ -389,8 +386,7 @@ struct GPT2Engine::Impl {
         for (void* p : pf_allocs) (void)hipFree(p);
         if (pf.host_ids) (void)hipHostFree(pf.host_ids);
         if (host_tokens) (void)hipHostFree(host_tokens);
-        if (host_topk_vals) (void)hipHostFree(host_topk_vals);
-        if (host_topk_idx) (void)hipHostFree(host_topk_idx);
+        if (host_topk_buf) (void)hipHostFree(host_topk_buf);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -757,15 +753,16 @@ void GPT2Engine::step(const int* tokens, int batch) {
 // reference's own route, the whole row to the host, with the same order for
 // equal values (lower index first) and the same draw.
 static int sample_top_k_engine(const float* d_logits, int V, int k, float temperature, unsigned seed,
-                               float* d_vals, int* d_idx, float* h_vals, int* h_idx, hipStream_t s) {
+                               float* d_buf, float* h_buf, hipStream_t s) {
     k = std::max(1, std::min(k, V));
     int token = 0;
     if (k <= ie::kTopkMax) {
-        if (ie_topk(1, d_logits, V, k, d_vals, d_idx, s) != IE_OK) throw std::runtime_error(ie_last_error());
-        HIPC(hipMemcpyAsync(h_vals, d_vals, sizeof(float) * k, hipMemcpyDeviceToHost, s));
-        HIPC(hipMemcpyAsync(h_idx, d_idx, sizeof(int) * k, hipMemcpyDeviceToHost, s));
+        // values in words [0, k), indices in [k, 2k): one copy back
+        if (ie_topk(1, d_logits, V, k, d_buf, reinterpret_cast<int*>(d_buf + k), s) != IE_OK)
+            throw std::runtime_error(ie_last_error());
+        HIPC(hipMemcpyAsync(h_buf, d_buf, sizeof(float) * 2 * k, hipMemcpyDeviceToHost, s));
         HIPC(hipStreamSynchronize(s));
-        if (ie_top_k_draw(h_vals, h_idx, k, temperature, seed, &token) != IE_OK)
+        if (ie_top_k_draw(h_buf, reinterpret_cast<const int*>(h_buf + k), k, temperature, seed, &token) != IE_OK)
             throw std::runtime_error(ie_last_error());
         return token;
     }
@@ -800,8 +797,8 @@ void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tok
         if (greedy) return I.host_tokens[0];
         const unsigned seed = first_pick ? 42u : ++sample_seed;
         first_pick = false;
-        return sample_top_k_engine(I.logits, I.cfg.vocab_size, top_k, temperature, seed, I.topk_vals, I.topk_idx,
-                                   I.host_topk_vals, I.host_topk_idx, I.stream);
+        return sample_top_k_engine(I.logits, I.cfg.vocab_size, top_k, temperature, seed, I.topk_buf,
+                                   I.host_topk_buf, I.stream);
     };
 
     const auto t_total = Clock::now();

@@ -63,22 +63,17 @@ int draw(const float* vals, const int* idx, int k, float temperature, float r) {
 
 // Device and pinned host buffers of the compat samplers, made on first use
 // and kept for the process (the reference allocates a host vector per call).
+// k values then k indices in one buffer, so one transfer brings both back.
 struct CompatBufs {
     std::mutex mu;
-    float* d_vals = nullptr;
-    int* d_idx = nullptr;
-    float* h_vals = nullptr;
-    int* h_idx = nullptr;
+    float* d_buf = nullptr;  // [2 kTopkMax] words
+    float* h_buf = nullptr;  // pinned copy
     bool ready() {
-        if (h_idx) return true;
-        if (!d_vals && hipMalloc(&d_vals, sizeof(float) * ie::kTopkMax) != hipSuccess) d_vals = nullptr;
-        if (!d_idx && hipMalloc(&d_idx, sizeof(int) * ie::kTopkMax) != hipSuccess) d_idx = nullptr;
-        if (!h_vals && hipHostMalloc(&h_vals, sizeof(float) * ie::kTopkMax, hipHostMallocDefault) != hipSuccess)
-            h_vals = nullptr;
-        if (d_vals && d_idx && h_vals &&
-            hipHostMalloc(&h_idx, sizeof(int) * ie::kTopkMax, hipHostMallocDefault) != hipSuccess)
-            h_idx = nullptr;
-        return h_idx != nullptr;  // what did succeed is kept for the next try
+        if (!d_buf && hipMalloc(&d_buf, sizeof(float) * 2 * ie::kTopkMax) != hipSuccess) d_buf = nullptr;
+        if (d_buf && !h_buf &&
+            hipHostMalloc(&h_buf, sizeof(float) * 2 * ie::kTopkMax, hipHostMallocDefault) != hipSuccess)
+            h_buf = nullptr;
+        return h_buf != nullptr;  // what did succeed is kept for the next try
     }
 };
 
@@ -112,12 +107,13 @@ int sample_argmax(const float* d_logits, int vocab_size) {
         ie::fail(IE_ERR_HIP, "sample_argmax: buffer allocation failed");
         return -1;
     }
-    if (ie_argmax(1, d_logits, vocab_size, b.d_idx, nullptr) != IE_OK) return -1;
-    if (hipMemcpy(b.h_idx, b.d_idx, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) {
+    int* d_idx = reinterpret_cast<int*>(b.d_buf);
+    if (ie_argmax(1, d_logits, vocab_size, d_idx, nullptr) != IE_OK) return -1;
+    if (hipMemcpy(b.h_buf, d_idx, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) {
         ie::fail(IE_ERR_HIP, "sample_argmax: copy failed");
         return -1;
     }
-    return b.h_idx[0];
+    return reinterpret_cast<const int*>(b.h_buf)[0];
 }
 
 // src/sampler.cu:16-45: k clamped to the vocabulary as there; the selection
@@ -130,13 +126,14 @@ int sample_top_k(const float* d_logits, int vocab_size, int k, float temperature
         ie::fail(IE_ERR_HIP, "sample_top_k: buffer allocation failed");
         return -1;
     }
-    if (ie_topk(1, d_logits, vocab_size, k, b.d_vals, b.d_idx, nullptr) != IE_OK) return -1;
-    if (hipMemcpy(b.h_vals, b.d_vals, sizeof(float) * k, hipMemcpyDeviceToHost) != hipSuccess ||
-        hipMemcpy(b.h_idx, b.d_idx, sizeof(int) * k, hipMemcpyDeviceToHost) != hipSuccess) {
+    if (ie_topk(1, d_logits, vocab_size, k, b.d_buf, reinterpret_cast<int*>(b.d_buf + k), nullptr) != IE_OK)
+        return -1;
+    if (hipMemcpy(b.h_buf, b.d_buf, sizeof(float) * 2 * k, hipMemcpyDeviceToHost) != hipSuccess) {
         ie::fail(IE_ERR_HIP, "sample_top_k: copy failed");
         return -1;
     }
     int token = -1;
-    if (ie_top_k_draw(b.h_vals, b.h_idx, k, temperature, seed, &token) != IE_OK) return -1;
+    if (ie_top_k_draw(b.h_buf, reinterpret_cast<const int*>(b.h_buf + k), k, temperature, seed, &token) != IE_OK)
+        return -1;
     return token;
 }

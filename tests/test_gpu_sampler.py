@@ -36,9 +36,13 @@ def test_topk_gpt2_rows(ie, orc, rows, k):
     check(ie, orc, x, k)
 
 
-@pytest.mark.parametrize("n,k", [(1, 1), (7, 7), (100, 100), (1023, 17), (8193, 1000), (70001, 333)])
+@pytest.mark.parametrize("n,k", [(1, 1), (2, 2), (3, 1), (5, 3), (7, 7), (100, 100), (1023, 17), (8193, 1000),
+                                 (65533, 40), (65534, 40), (70001, 333)])
 def test_topk_shapes(ie, orc, n, k):
-    x = rng(n + k).standard_normal((2, n)).astype(np.float32)
+    """Three rows, so rows 1 and 2 start inside a 16-byte chunk when n is not
+    a multiple of 4 (n <= 5: no whole chunk at all); 65533 is the longest row
+    held in registers, 65534 the shortest streamed one."""
+    x = rng(n + k).standard_normal((3, n)).astype(np.float32)
     check(ie, orc, x, k)
 
 
