@@ -18,7 +18,8 @@ inputs.  The same JSON line carries:
   sampler       top-k sampling: device selection kernel, one sample_top_k
                 call, the reference's whole-row copy, sampled decode at batch 1
   cpu_baseline  the C oracle (oracle/liborc.so) on a bounded sample of the
-                8192^3 GEMM, on this host's cores
+                8192^3 GEMM, on this host's cores; cpu_baseline_attn the same
+                for decode attention cfg4 ctx 8192 fp32
   traffic       HBM bytes per launch of the dominant kernels (rocprofv3
                 FETCH_SIZE / WRITE_SIZE passes, calibrated on a 1 GiB copy)
 Kernel durations come from HIP events on the stream the kernels run on.
@@ -505,6 +506,45 @@ def cpu_baseline(inputs, budget_s=12.0):
                       f"+ dequant, OpenMP over rows, {dt:.1f} s"}
 
 
+def cpu_baseline_attn(B=32, ctx=8192, seed=8192, budget_s=8.0):
+    """The oracle's decode attention (the reference's split-K algorithm in fp64,
+    tests/test_paged_attention.cu:138-179 as the BASELINE plan restates it),
+    OpenMP over (sequence, query head), on the cfg4 ctx 8192 fp32 workload
+    (same shapes and length law; U(-1,1) data), repeated until budget_s of
+    timed work."""
+    import numpy as np
+
+    from oracle import orc
+
+    H_q, H_kv, d, bs = 32, 8, 128, 16
+    r = np.random.default_rng(seed)
+    lens = r.integers(ctx // 2, ctx + 1, B).astype(np.int32)
+    nbs = (lens + bs - 1) // bs
+    P, nbps = int(nbs.sum()), int(nbs.max())
+    kc = r.random((P, bs, H_kv, d), dtype=np.float32) * 2 - 1
+    vc = r.random((P, bs, H_kv, d), dtype=np.float32) * 2 - 1
+    perm = r.permutation(P).astype(np.int32)
+    table = np.zeros((B, nbps), np.int32)
+    off = 0
+    for b in range(B):
+        table[b, : nbs[b]] = perm[off: off + nbs[b]]
+        off += int(nbs[b])
+    Q = r.random((B, H_q, d), dtype=np.float32) * 2 - 1
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    orc.set_threads(threads)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.decode_attn(Q, kc, vc, table, lens, int(lens.max()), bs, H_kv)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            break
+    alg = int(lens.sum()) * H_kv * d * 2 * 4 + 2 * B * H_q * d * 4 + 4 * P + 4 * B
+    return {"value": round(alg * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"decode attention cfg4 ctx {ctx} fp32, {B} sequences (Σctx {int(lens.sum())}), the "
+                      f"oracle's fp64 split-K restatement, OpenMP over (sequence, head), {reps} calls in {dt:.1f} s"}
+
+
 def main():
     args = parse()
     if args.pmc_child:
@@ -567,6 +607,8 @@ def main():
     if "cpu" not in skip:
         log("cpu baseline")
         res["cpu_baseline"] = cpu_baseline(h["inputs"])
+        res["cpu_baseline_attn"] = cpu_baseline_attn()
+        log(f"cpu attention {res['cpu_baseline_attn']}")
     if not args.no_traffic:
         log("traffic (rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
         t = measure_traffic()
