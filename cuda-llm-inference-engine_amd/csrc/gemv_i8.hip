@@ -18,6 +18,8 @@
 //     rotations (no LDS round trip), then lane m of the row stores output m.
 // Requires K % 16 == 0 and 16-byte aligned A/BT; other shapes use the generic
 // kernel at the end of this file.
+#include <algorithm>
+
 #include "device_util.h"
 #include "epilogue.h"
 #include "ie_internal.h"
@@ -342,8 +344,11 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
 // C[4 * (l / 16) + v][n0 + l % 16].  For K <= 4096 the activation block is
 // staged in LDS (or built there by the fused prologue); beyond that each lane
 // reads its A fragment straight from global memory (the block is L2-resident).
-// Weight loads run U steps ahead of the MFMAs.
-template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false>
+// Weight loads run U steps ahead of the MFMAs.  With the activations read
+// from global memory (K > 4096), NG groups of 16 output features share each
+// activation fragment: one A load feeds NG MFMAs, so the activations cost
+// 1/NG of the weights' L2 and address traffic instead of as much again.
+template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false, int NG = 1>
 __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
     int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
@@ -353,15 +358,18 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
     constexpr int KW = K64 / 4;                // K steps per wave
     constexpr bool A_LDS = K <= 4096;
     static_assert(A_LDS || SRC == kSrcInt8, "fused prologues stage A in LDS");
-    // weight loads in flight per lane: the largest divisor of KW up to 8
-    constexpr int U = KW <= 8 ? KW : KW % 8 == 0 ? 8 : KW % 6 == 0 ? 6 : KW % 4 == 0 ? 4 : 2;
+    static_assert(NG == 1 || (!A_LDS && EPI != kEpiQKV), "feature groups share global activations");
+    // weight steps in flight per lane: the largest divisor of KW up to 8
+    // (up to 4 with several feature groups, whose loads multiply by NG)
+    constexpr int UMAX = NG > 1 ? 4 : 8;
+    constexpr int U = KW <= UMAX ? KW : KW % UMAX == 0 ? UMAX : KW % 6 == 0 && UMAX >= 6 ? 6 : KW % 4 == 0 ? 4 : 2;
     static_assert(KW % U == 0, "whole batches");
     __shared__ i32x4 a_lds[A_LDS ? 16 * K / 16 : 1];
     __shared__ float s_sa[16];
-    __shared__ i32x4 red[3][64];
+    __shared__ i32x4 red[3][NG][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, kq = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * NG;
     const int kb = wave * KW;  // first K step of this wave
 
     auto ldw = [&](const int8_t* p) {
@@ -372,20 +380,26 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
     };
     // Epilogue operands of this lane's outputs (rows 4 kq + v, column n0 +
     // col; only wave 0 stores) requested ahead of the weights.
-    EpiIn ein[4];
+    EpiIn ein[NG][4];
     size_t slot[16];
     if (wave == 0) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-            ein[v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(n0 + col, N - 1), N, sB, bias, residual);
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                ein[g][v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(n0 + 16 * g + col, N - 1), N, sB, bias,
+                                          residual);
         if constexpr (EPI == kEpiQKV) qkv_slots<16>(f, M, slot);
     }
-    const int8_t* w = BT + (size_t)min(n0 + col, N - 1) * K + kq * 16;
+    const int8_t* w[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) w[g] = BT + (size_t)min(n0 + 16 * g + col, N - 1) * K + kq * 16;
     const int8_t* arow = A + (size_t)min(col, M - 1) * K + kq * 16;  // global A (K > 4096)
-    i32x4 wv[U], ag[A_LDS ? 1 : U];
+    i32x4 wv[U][NG], ag[A_LDS ? 1 : U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        wv[u] = ldw(w + (size_t)(kb + u) * 64);
+#pragma unroll
+        for (int g = 0; g < NG; ++g) wv[u][g] = ldw(w[g] + (size_t)(kb + u) * 64);
         if constexpr (!A_LDS) ag[u] = *reinterpret_cast<const i32x4*>(arow + (size_t)(kb + u) * 64);
     }
 
@@ -426,41 +440,55 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
 
     // Two accumulators alternate so consecutive MFMAs do not wait on each
     // other; their integer sum is exact.
-    i32x4 acc = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    i32x4 acc[NG], acc1[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) acc[g] = acc1[g] = i32x4{0, 0, 0, 0};
 #pragma unroll 1
     for (int k0 = 0; k0 < KW; k0 += U) {
-        i32x4 av[U], cur[U];
+        i32x4 av[U], cur[U][NG];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if constexpr (A_LDS)
                 av[u] = a_lds[col * (K / 16) + (kb + k0 + u) * 4 + kq];
             else
                 av[u] = ag[u];
-            cur[u] = wv[u];
+#pragma unroll
+            for (int g = 0; g < NG; ++g) cur[u][g] = wv[u][g];
         }
         // next batch's weights (and global A fragments) in flight during the MFMAs
         if (k0 + U < KW) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                wv[u] = ldw(w + (size_t)(kb + k0 + U + u) * 64);
+#pragma unroll
+                for (int g = 0; g < NG; ++g) wv[u][g] = ldw(w[g] + (size_t)(kb + k0 + U + u) * 64);
                 if constexpr (!A_LDS) ag[u] = *reinterpret_cast<const i32x4*>(arow + (size_t)(kb + k0 + U + u) * 64);
             }
         }
 #pragma unroll
-        for (int u = 0; u < U; u += 2) {
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u], cur[u], acc, 0, 0, 0);
-            if (u + 1 < U)
-                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u + 1], cur[u + 1], acc1, 0, 0, 0);
-        }
+        for (int u = 0; u < U; u += 2)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                acc[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u], cur[u][g], acc[g], 0, 0, 0);
+                if (u + 1 < U)
+                    acc1[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u + 1], cur[u + 1][g], acc1[g], 0, 0, 0);
+            }
     }
-    acc += acc1;
-    if (wave > 0) red[wave - 1][lane] = acc;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        acc[g] += acc1[g];
+        if (wave > 0) red[wave - 1][g][lane] = acc[g];
+    }
     __syncthreads();
     if (wave > 0) return;
-    acc += red[0][lane];
-    acc += red[1][lane];
-    acc += red[2][lane];
-    const int n = n0 + col;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        acc[g] += red[0][g][lane];
+        acc[g] += red[1][g][lane];
+        acc[g] += red[2][g][lane];
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+    const int n = n0 + 16 * g + col;
     if (n < N) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -474,8 +502,113 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
                     for (int q = 0; q < 4; ++q)
                         if (kq == q) sl = slot[4 * q + v];
                 }
-                gemv_store<EPI>(C, m, n, N, acc[v], sa, ein[v], sl, f);
+                gemv_store<EPI>(C, m, n, N, acc[g][v], sa, ein[g][v], sl, f);
             }
+        }
+    }
+    }
+}
+
+// K = 8192, 2 <= M <= 16: the MFMA GEMV made persistent.  One workgroup per
+// CU stages the 16 x K activation block (rows past M repeat row M - 1) in LDS
+// once, 128 KiB, and walks 16-feature groups g = blockIdx.x, + gridDim.x, ...;
+// its four waves split each group's K four ways and add their int32 tiles in
+// LDS (exact), as the per-group kernel does.  The activations cost 32 MiB of
+// L2 reads in all instead of as much as the weights, and each wave's weight
+// loads run U steps ahead across group boundaries, so the stream does not
+// drain between groups.
+template <int EPI, int K64, bool NT, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_i8_mfma16_persist_kernel(
+    int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT, const float* __restrict__ sA,
+    const float* __restrict__ sB, const float* bias, const float* residual, void* C) {
+    constexpr int K = K64 * 64;
+    constexpr int KW = K64 / NW;  // K steps per wave and group
+    constexpr int U = 8;          // weight steps in flight per lane
+    static_assert(KW % U == 0, "whole batches per group");
+    constexpr int NB = KW / U;   // batches per group
+    __shared__ i32x4 a_lds[16 * K / 16];
+    __shared__ i32x4 red[NW - 1][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, kq = lane >> 4;
+    const int kb = wave * KW;
+    const int ngroups = (N + 15) / 16;
+    const int mine = (int)blockIdx.x < ngroups ? (ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    const int nbat = mine * NB;
+
+    auto ldw = [&](const int8_t* p) {
+        if constexpr (NT)
+            return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+        else
+            return *reinterpret_cast<const i32x4*>(p);
+    };
+    // weights of batch bi: group blockIdx.x + (bi / NB) gridDim.x, steps
+    // kb + (bi % NB) U .. + U
+    auto wrow = [&](int bi) {
+        const int g = (int)blockIdx.x + (bi / NB) * (int)gridDim.x;
+        return BT + (size_t)min(g * 16 + col, N - 1) * K + kq * 16 + (size_t)(kb + (bi % NB) * U) * 64;
+    };
+    i32x4 wv[U];
+    if (nbat > 0) {
+        const int8_t* w = wrow(0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) wv[u] = ldw(w + (size_t)u * 64);
+    }
+    for (int i = threadIdx.x; i < 16 * (K / 16); i += 64 * NW) {
+        const int m = i / (K / 16);
+        a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)min(m, M - 1) * K)[i - m * (K / 16)];
+    }
+    __syncthreads();
+
+    i32x4 acc = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    EpiIn ein[4];
+#pragma unroll 1
+    for (int bi = 0; bi < nbat; ++bi) {
+        const int g = (int)blockIdx.x + (bi / NB) * (int)gridDim.x;
+        if (bi % NB == 0 && wave == 0) {
+            // the group's epilogue operands, requested with its first weights
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                ein[v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(g * 16 + col, N - 1), N, sB, bias, residual);
+        }
+        i32x4 cur[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) cur[u] = wv[u];
+        if (bi + 1 < nbat) {  // next batch, possibly the next group's, in flight
+            const int8_t* w = wrow(bi + 1);
+#pragma unroll
+            for (int u = 0; u < U; ++u) wv[u] = ldw(w + (size_t)u * 64);
+        }
+        const int kk = kb + (bi % NB) * U;
+#pragma unroll
+        for (int u = 0; u < U; u += 2) {
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_lds[col * (K / 16) + (kk + u) * 4 + kq], cur[u], acc, 0,
+                                                        0, 0);
+            acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_lds[col * (K / 16) + (kk + u + 1) * 4 + kq], cur[u + 1],
+                                                         acc1, 0, 0, 0);
+        }
+        if (bi % NB == NB - 1) {  // group done (uniform across the workgroup)
+            acc += acc1;
+            if (wave > 0) red[wave - 1][lane] = acc;
+            __syncthreads();
+            if (wave == 0) {
+#pragma unroll
+                for (int w = 0; w < NW - 1; ++w) acc += red[w][lane];
+                const int n = g * 16 + col;
+                if (n < N) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int m = 4 * kq + v;
+                        if (m < M) {
+                            float sa = 0.0f;
+                            if constexpr (EPI != IE_EPI_I32) sa = sA[m];
+                            gemv_store<EPI>(C, m, n, N, acc[v], sa, ein[v], 0, GemvFusion{});
+                        }
+                    }
+                }
+            }
+            __syncthreads();  // red is rewritten by the next group
+            acc = i32x4{0, 0, 0, 0};
+            acc1 = i32x4{0, 0, 0, 0};
         }
     }
 }
@@ -528,14 +661,24 @@ void launch_fixed(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFu
             a.M, a.N, a.A, a.BT, a.sA, a.sB, a.bias, a.residual, a.C, f);
 }
 
-template <int EPI, int K64, int SRC = kSrcInt8>
+template <int EPI, int K64, int SRC = kSrcInt8, int NG = 1>
 void launch_mfma16(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFusion{}) {
-    const unsigned blocks = (unsigned)((a.N + 15) / 16);
+    const unsigned blocks = (unsigned)((a.N + 16 * NG - 1) / (16 * NG));
     const bool nt = (size_t)a.N * K64 * 64 >= kStreamWeightBytes;
-    auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true> : gemv_i8_mfma16_kernel<EPI, K64, SRC, false>;
+    auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true, NG> : gemv_i8_mfma16_kernel<EPI, K64, SRC, false, NG>;
     k<<<blocks, 256, 0, s>>>(a.M, a.N, reinterpret_cast<const int8_t*>(a.A),
                              reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual,
                              a.C, f);
+}
+
+template <int EPI, int K64>
+void launch_mfma16_persist(const GemmArgs& a, hipStream_t s) {
+    constexpr int NW = 8;  // 8 waves split each group's K: measured ahead of 4 and 16
+    const unsigned blocks = (unsigned)std::min((a.N + 15) / 16, num_cus());
+    const bool nt = (size_t)a.N * K64 * 64 >= kStreamWeightBytes;
+    auto* k = nt ? gemv_i8_mfma16_persist_kernel<EPI, K64, true, NW> : gemv_i8_mfma16_persist_kernel<EPI, K64, false, NW>;
+    k<<<blocks, 64 * NW, 0, s>>>(a.M, a.N, reinterpret_cast<const int8_t*>(a.A),
+                                         reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
 }
 
 template <int EPI, int K, int SRC>
@@ -556,8 +699,17 @@ void launch_mt(const GemmArgs& a, hipStream_t s) {
     // work per pass (no cross-pass prefetch at this K) outlasts the loads, so
     // the MFMA kernel takes over.
     if (a.K == 8192) {
-        if constexpr (MT == 1) return launch_fixed<1, EPI, 512>(a, s);
-        else return launch_mfma16<EPI, 128>(a, s);
+        if constexpr (MT == 1) {
+            return launch_fixed<1, EPI, 512>(a, s);
+        } else {
+            // Measured at N = 8192 and 28672, M = 2..16 (fraction of HBM peak):
+            // many groups and M >= 5, the persistent kernel (N = 28672, M = 16:
+            // 0.48 -> 0.60); around N = 8192, two feature groups per workgroup
+            // (M = 16: 0.41 -> 0.49, M = 2: 0.53 -> 0.57); otherwise one.
+            if (a.N >= 16384 && a.M >= 5) return launch_mfma16_persist<EPI, 128>(a, s);
+            if (a.N >= 8192 && a.N < 16384) return launch_mfma16<EPI, 128, kSrcInt8, 2>(a, s);
+            return launch_mfma16<EPI, 128>(a, s);
+        }
     }
     // Specialised K: the GPT-2 widths.
     if constexpr (MT <= 4) {

@@ -97,6 +97,33 @@ def test_i32_odd_shapes(ie, orc, M, N, K, path):
     i32_case(ie, orc, M, N, K, path, M + N + K + path)
 
 
+@pytest.mark.parametrize("M,N", [(2, 8200), (7, 8200), (16, 8192), (8, 4096), (4, 28672), (5, 16400),
+                                 (13, 16400), (16, 28672)])
+def test_i32_gemv_k8192_paths(ie, orc, M, N):
+    """K = 8192 decode GEMV dispatch: one or two 16-feature groups per workgroup
+    (N below 16384) and the persistent kernel (N >= 16384, M >= 5), with partial
+    last groups (N % 16 != 0 only for N = 8200, 16400) and M not a multiple of 4."""
+    i32_case(ie, orc, M, N, 8192, ie.PATH_GEMV, M * 3 + N)
+
+
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_persistent_gemv_epilogues(ie, orc, epi):
+    M, N, K = 13, 16400, 8192
+    A, W = problem(M, N, K, 77 + epi)
+    r = rng(6 + epi)
+    bias = (r.standard_normal(N) * 0.5).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi,
+                            dev(bias) if epi else None, dev(res) if epi == 3 else None, path=ie.PATH_GEMV))
+    want = orc.gemm(Ap, Wp, sA, sW, epi, bias if epi else None, res if epi == 3 else None)
+    if epi == 2:
+        assert np.allclose(got, want, rtol=2e-6, atol=1e-7), np.abs(got - want).max()
+    else:
+        assert np.array_equal(got, want), np.abs(got - want).max()
+
+
 # ------------------------------------------------------------------ epilogues
 @pytest.mark.parametrize("M,K,N,path", [(1, 768, 2304, 1), (16, 3072, 768, 1), (4, 768, 3072, 1),
                                         (64, 768, 2304, 2), (512, 3072, 768, 2), (16, 768, 768, 2)])
