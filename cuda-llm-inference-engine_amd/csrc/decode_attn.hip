@@ -818,6 +818,8 @@ constexpr long long kWaveSplitUnits = 1024;
 // Batches up to this size use the balanced partition for one-wave splits
 // (every workgroup scans the context lengths twice).
 constexpr int kBalancedMaxB = 4096;
+// At most this many (b, kv head, split) units count as few.
+constexpr long long kFewUnits = 64;
 
 // Workgroups of `threads` threads of kernel f resident per CU (at least 1),
 // looked up once per kernel.
@@ -876,11 +878,23 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
                                            a.num_blocks_per_seq, a.num_splits, nbmax, qscale, a.workspace);
         return;
     }
-    auto* k = wave ? (bs16 ? decode_attn_split_kernel<D, G, KV, 1, true, RW, NTW>
-                           : decode_attn_split_kernel<D, G, KV, 1, false, RW, NTW>)
-                   : (bs16 ? decode_attn_split_kernel<D, G, KV, 4, true, 2, 256>
-                           : decode_attn_split_kernel<D, G, KV, 4, false, 2, 256>);
-    k<<<grid, wave ? 64 * hw : 256, 0, s>>>(
+    // Few units (GPT-2 at batch 1: 12 heads, one split): 8 waves share each
+    // split, so a wave walks half as many chunks one after another; measured
+    // +2.4% decode tok/s at batch 1 (16 waves: +1%), where it fits without
+    // spilling (G <= 4).
+    constexpr int WF = 8;
+    constexpr bool WF_FITS = G <= 4;
+    const bool few = WF_FITS && !wave && (long long)a.num_splits * a.H_kv * a.B <= kFewUnits;
+    using KernelT = decltype(&decode_attn_split_kernel<D, G, KV, 4, true, 2, 256>);
+    KernelT k = wave ? (bs16 ? decode_attn_split_kernel<D, G, KV, 1, true, RW, NTW>
+                             : decode_attn_split_kernel<D, G, KV, 1, false, RW, NTW>)
+                     : (bs16 ? decode_attn_split_kernel<D, G, KV, 4, true, 2, 256>
+                             : decode_attn_split_kernel<D, G, KV, 4, false, 2, 256>);
+    if constexpr (WF_FITS)
+        if (few)
+            k = bs16 ? decode_attn_split_kernel<D, G, KV, WF, true, 2, 64 * WF>
+                     : decode_attn_split_kernel<D, G, KV, WF, false, 2, 64 * WF>;
+    k<<<grid, wave ? 64 * hw : few ? 64 * WF : 256, 0, s>>>(
         a.Q, static_cast<const KV*>(a.k_cache), static_cast<const KV*>(a.v_cache),
         a.block_table, a.context_lens, a.H_q, a.H_kv, a.block_size, a.num_blocks_per_seq,
         a.num_splits, a.blocks_per_split, qscale, a.workspace, a.O);

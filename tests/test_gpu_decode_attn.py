@@ -149,10 +149,11 @@ def test_explicit_split_counts(ie, orc, splits):
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
 def test_one_wave_and_four_wave_splits(ie, orc, G, d, kvdt):
-    """Splits of >= 256 tokens run on one wave each, shorter ones on four waves
-    that merge in LDS: both layouts for every head width, group size and KV
-    type (max_context_len 700: 1 and 2 splits are one-wave, 3 and 11 are
-    four-wave)."""
+    """Splits of >= 256 tokens run on one wave each, shorter ones on several
+    waves that merge in LDS: both layouts for every head width, group size and
+    KV type (max_context_len 700: 1 and 2 splits are one-wave, 3 and 11 are
+    multi-wave; with these few (b, head, split) units, eight waves per split
+    for G <= 4, four for G = 8)."""
     r = rng(1000 + 10 * G + d + kvdt)
     B, H_kv = 2, 2
     H_q = H_kv * G
@@ -165,6 +166,24 @@ def test_one_wave_and_four_wave_splits(ie, orc, G, d, kvdt):
     for splits in (1, 2, 3, 11):
         got = run_gpu(ie, Q, kc, vc, table, lens, 700, 16, H_kv, kv_dtype=kvdt, splits=splits)
         assert rel_err(got, want) < REL, splits
+
+
+@pytest.mark.parametrize("kvdt", [0, 1])
+@pytest.mark.parametrize("G", [1, 4])
+def test_four_wave_splits_with_many_units(ie, orc, G, kvdt):
+    """More than 64 (b, head, split) units of short splits (under 256 tokens
+    each): four waves per split (B 8 x 4 KV heads x 3 splits = 96 units)."""
+    r = rng(1100 + G + kvdt)
+    B, H_kv, d = 8, 4, 64
+    lens = r.integers(100, 701, B)
+    kc, vc, table, _, _ = make_paged_cache(r, B, H_kv, d, lens, 16)
+    Q = r.standard_normal((B, H_kv * G, d)).astype(np.float32)
+    if kvdt:
+        kc, vc = bf16_bits(kc), bf16_bits(vc)
+    mx = int(lens.max())
+    want = orc.decode_attn(Q, kc, vc, table, lens, mx, 16, H_kv, kv_dtype=kvdt)
+    got = run_gpu(ie, Q, kc, vc, table, lens, mx, 16, H_kv, kv_dtype=kvdt, splits=3)
+    assert rel_err(got, want) < REL
 
 
 def test_edges(ie, orc):
