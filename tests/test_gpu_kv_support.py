@@ -114,6 +114,23 @@ def test_embedding_vocab_argmax(ie, orc):
     assert host(ie.argmax(dev(tie))).tolist() == [5, 0]
 
 
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 7, 4096, 50257, 70001])
+def test_argmax_rows_and_ties(ie, orc, n):
+    """First index of the maximum (std::max_element) per row: three rows, so
+    rows 1 and 2 start inside a 16-byte chunk when n is not a multiple of 4;
+    the maximum repeated later in a row, in the first and the last element,
+    and an all -inf row."""
+    r = rng(n)
+    x = r.standard_normal((3, n)).astype(np.float32)
+    if n > 2:
+        x[0, n // 3] = x[0, n - 1] = 9.0
+        x[1, 0] = 9.0
+        x[1, n - 1] = 9.0
+    x[2, :] = -np.inf
+    got = host(ie.argmax(dev(x))).tolist()
+    assert got == [orc.argmax(x[i]) for i in range(3)] == [int(np.argmax(x[i])) for i in range(3)]
+
+
 @pytest.mark.parametrize("d,V", [(768, 50257), (128, 1000), (1024, 333), (100, 77)])
 def test_vocab_proj_rows_bit_identical_across_batch(ie, orc, d, V):
     """Row r of a 16-row projection equals the 1-row and 5-row projections of
