@@ -9,15 +9,16 @@
 //     4x4 blocks of v_mfma_i32_32x32x32_i8 (256 int32 accumulators per lane,
 //     held in AGPRs), so every 16-byte A or B fragment read from LDS feeds
 //     four MFMAs;
-//   * K advances 128 bytes per stage; a stage is 2 x 256 rows x 128 B = 64 KiB
-//     and two stages (128 KiB of the 160 KiB LDS) double-buffer the loop;
+//   * K advances 64 bytes per stage; a stage is 2 x 256 rows x 64 B = 32 KiB
+//     and a ring of four stages (128 KiB of the 160 KiB LDS) keeps three in
+//     flight while one is read;
 //   * global -> LDS copies use global_load_lds_dwordx4 (16 B per lane straight
 //     into LDS, no VGPR round trip); a wave-load fills 1 KiB = 8 rows, the
 //     lane -> global address map applies the LDS swizzle, so the fixed
 //     lane-ordered LDS destination lands each 16-byte chunk at its swizzled
 //     slot;
-//   * LDS rows are 128 B with 16-byte chunk c of row r stored at slot
-//     c ^ ((r >> 1) & 7), which spreads the 32 rows an MFMA operand read
+//   * LDS rows are 64 B with 16-byte chunk c of row r stored at slot
+//     c ^ ((r >> 2) & 3) (swz), which spreads the rows an MFMA operand read
 //     touches over all banks;
 //   * workgroup ids are remapped so each XCD (ids = xcd mod 8) receives a
 //     contiguous run of tiles, walked in groups of GROUP_M tile rows, so the
