@@ -5,10 +5,11 @@
 // 14_int8_gemm.cu:65-170): exact int32 K-sum, then the dequant epilogue.
 //
 // MI355X mapping:
-//   * 256x256 C tile per 256-thread workgroup; each wave owns 128x128 as
-//     4x4 blocks of v_mfma_i32_32x32x32_i8 (256 int32 accumulators per lane,
-//     held in AGPRs), so every 16-byte A or B fragment read from LDS feeds
-//     four MFMAs;
+//   * 256x256 C tile per 512-thread workgroup; each of the 2 x 4 waves owns
+//     128x64 as 4x2 blocks of v_mfma_i32_32x32x32_i8 (128 int32 accumulators
+//     per lane), two waves per SIMD so one's MFMAs run while the other waits
+//     at the stage barrier; each 16-byte A fragment read from LDS feeds two
+//     MFMAs, each B fragment four (a 4-wave 128x128 layout is kept as NW = 4);
 //   * K advances 64 bytes per stage; a stage is 2 x 256 rows x 64 B = 32 KiB
 //     and a ring of four stages (128 KiB of the 160 KiB LDS) keeps three in
 //     flight while one is read;
@@ -36,10 +37,9 @@ constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int NSTAGE = 4;              // LDS ring depth
 constexpr int OPER = BM * BK;          // bytes of one operand tile per stage
 constexpr int STAGE = 2 * OPER;        // A + B
-constexpr int GROUP_M = 4;
+constexpr int GROUP_M = 4;             // measured ahead of 2, 8 and 16
 constexpr int CHUNKS = BK / 16;        // 16-byte chunks per LDS row
 constexpr int ROWS_PER_LOAD = 64 / CHUNKS;          // rows one wave-load fills
-constexpr int LOADS_PER_WAVE = BM / ROWS_PER_LOAD / 4;  // per operand per stage
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
@@ -64,8 +64,11 @@ __device__ __forceinline__ i32x4 read_frag(const int8_t* lds_oper, int row, int 
     return *reinterpret_cast<const i32x4*>(lds_oper + row * BK + ((chunk ^ swz(row)) << 4));
 }
 
-template <int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
+// NW = 4: 2 x 2 waves of 128 x 128 (one wave per SIMD); NW = 8: 2 x 4 waves
+// of 128 x 64 (two per SIMD, so one wave's MFMAs can run while the other
+// waits at the stage barrier or for its copies).
+template <int EPI, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     int M, int N, int K, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
     const float* residual, void* C, int tiles_m, int tiles_n) {
@@ -84,15 +87,18 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
     const int tn = in_group / gm;
     const int m0 = tm * BM, n0 = tn * BN;
 
+    constexpr int WN = NW / 2;              // waves across N
+    constexpr int NJ = 4 / (NW / 4);        // 32-column blocks per wave: 4 or 2
+    constexpr int LOADS_PER_WAVE = BM / ROWS_PER_LOAD / NW;  // per operand per stage
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
 
-    i32x16 acc[4][4];
+    i32x16 acc[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
@@ -125,18 +131,18 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
     // stage, slot 1 = k-substep 1.  An MFMA blocks instruction issue until the
     // matrix pipe takes it, so LDS reads and global copies are interleaved one
     // per MFMA (sched_group_barrier) to run in the shadow of the matrix work.
-    i32x4 af[2][4], bf[2][4];
+    i32x4 af[2][4], bf[2][NJ];
     auto frags = [&](const int8_t* sa, const int8_t* sb, int ks, int slot) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[slot][i] = read_frag(sa, wm * 128 + i * 32 + frow, ks * 2 + fchunk);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[slot][j] = read_frag(sb, wn * 128 + j * 32 + frow, ks * 2 + fchunk);
+        for (int j = 0; j < NJ; ++j) bf[slot][j] = read_frag(sb, wn * 32 * NJ + j * 32 + frow, ks * 2 + fchunk);
     };
     auto mfma_rows = [&](int slot, int i0, int i1) {
 #pragma unroll
         for (int i = i0; i < i1; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
     };
     frags(lds, lds + OPER, 0, 0);
@@ -150,8 +156,10 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
         issue(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
         frags(sa, sb, 1, 1);
         mfma_rows(0, 0, 4);
+        // 4 NJ MFMAs, 4 + NJ LDS reads, 2 LOADS_PER_WAVE copies: one read or
+        // copy after each MFMA
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
+        for (int g = 0; g < 2 * NJ; ++g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -175,7 +183,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
         }
         mfma_rows(1, 2, 4);
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
+        for (int g = 0; g < 2 * NJ; ++g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
@@ -189,8 +197,38 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
     // of column l % 32.
     const int h = lane >> 5;
     const int rbase = m0 + wm * 128 + 4 * h;
-    const int cbase = n0 + wn * 128 + (lane & 31);
-    float sa[4][16], sb[4];
+    const int cbase = n0 + wn * 32 * NJ + (lane & 31);
+    if constexpr (NW == 8 && EPI != IE_EPI_I32) {
+        // two waves per SIMD leave no room for all 64 row scales beside the
+        // accumulators: gather them one 32-row block at a time
+        float sb[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) sb[j] = sB[min(cbase + j * 32, N - 1)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sa[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sa[v] = sA[min(rbase + i * 32 + 8 * (v >> 2) + (v & 3), M - 1)];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) asm volatile("" ::"v"(sa[v]));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) asm volatile("" ::"v"(sb[j]));
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
+                if (m >= M) continue;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const int n = cbase + j * 32;
+                    if (n < N)
+                        store_epilogue<EPI, true>(C, (size_t)m * N + n, acc[i][j][v], sa[v], sb[j], bias, residual,
+                                                  n);
+                }
+            }
+        }
+        return;
+    }
+    float sa[4][16], sb[NJ];
     if constexpr (EPI != IE_EPI_I32) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -198,7 +236,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
             for (int v = 0; v < 16; ++v)
                 sa[i][v] = sA[min(rbase + i * 32 + 8 * (v >> 2) + (v & 3), M - 1)];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sb[j] = sB[min(cbase + j * 32, N - 1)];
+        for (int j = 0; j < NJ; ++j) sb[j] = sB[min(cbase + j * 32, N - 1)];
         // Consume every scale once in straight-line code: the compiler waits
         // for the loads here, once.  Otherwise the branchy store loop below gets
         // a conservative vmcnt(0) before each store, and since vmcnt also counts
@@ -208,7 +246,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
 #pragma unroll
             for (int v = 0; v < 16; ++v) asm volatile("" ::"v"(sa[i][v]));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) asm volatile("" ::"v"(sb[j]));
+        for (int j = 0; j < NJ; ++j) asm volatile("" ::"v"(sb[j]));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -217,7 +255,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_256_kernel(
             const int m = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
             if (m >= M) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < NJ; ++j) {
                 const int n = cbase + j * 32;
                 if (n < N)
                     store_epilogue<EPI, true>(C, (size_t)m * N + n, acc[i][j][v], sa[i][v], sb[j], bias,
@@ -231,7 +269,10 @@ template <int EPI>
 struct BigLaunch {
     static void run(const GemmArgs& a, hipStream_t s) {
         const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
-        gemm_i8_256_kernel<EPI><<<tm * tn, 256, 0, s>>>(
+        // 8 waves: 2231-2240 TOP/s steady state against 2153 with 4 (same box,
+        // bit-identical C)
+        constexpr int NW = 8;
+        gemm_i8_256_kernel<EPI, NW><<<tm * tn, 64 * NW, 0, s>>>(
             a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
             a.sA, a.sB, a.bias, a.residual, a.C, tm, tn);
     }
