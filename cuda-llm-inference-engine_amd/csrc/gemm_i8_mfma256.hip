@@ -10,21 +10,21 @@
 //     per lane), two waves per SIMD so one's MFMAs run while the other waits
 //     at the stage barrier; each 16-byte A fragment read from LDS feeds two
 //     MFMAs, each B fragment four (a 4-wave 128x128 layout is kept as NW = 4);
-//   * K advances 64 bytes per stage; a stage is 2 x 256 rows x 64 B = 32 KiB
-//     and a ring of four stages (128 KiB of the 160 KiB LDS) keeps three in
-//     flight while one is read;
+//   * K advances 128 bytes per stage; a stage is 2 x 256 rows x 128 B = 64 KiB
+//     and two stages (128 KiB of the 160 KiB LDS) alternate: one stage's
+//     copies in flight while the other is read (four k-substeps of 32 B);
 //   * global -> LDS copies use global_load_lds_dwordx4 (16 B per lane straight
 //     into LDS, no VGPR round trip); a wave-load fills 1 KiB = 8 rows, the
 //     lane -> global address map applies the LDS swizzle, so the fixed
 //     lane-ordered LDS destination lands each 16-byte chunk at its swizzled
 //     slot;
-//   * LDS rows are 64 B with 16-byte chunk c of row r stored at slot
-//     c ^ ((r >> 2) & 3) (swz), which spreads the rows an MFMA operand read
+//   * LDS rows are 128 B with 16-byte chunk c of row r stored at slot
+//     c ^ ((r >> 1) & 7) (swz), which spreads the rows an MFMA operand read
 //     touches over all banks;
 //   * workgroup ids are remapped so each XCD (ids = xcd mod 8) receives a
 //     contiguous run of tiles, walked in groups of GROUP_M tile rows, so the
 //     workgroups resident on one XCD share A and B panels in its L2.
-// Requirements (checked by the launcher): K % 64 == 0, 16-byte aligned A/BT.
+// Requirements (checked by the launcher): K % 128 == 0, 16-byte aligned A/BT.
 // Rows past M or N read the last valid row (no fault, results discarded).
 #include "device_util.h"
 #include "epilogue.h"
@@ -33,8 +33,11 @@
 namespace ie {
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int NSTAGE = 4;              // LDS ring depth
+// 128-byte stages, two of them (128 KiB of LDS): one stage's copies in flight
+// while the other is computed, with half the barriers of 64-byte stages in a
+// four-deep ring (2396 against 2266 TOP/s at 8192^3, same box, same bits).
+constexpr int BM = 256, BN = 256, BK = 128;
+constexpr int NSTAGE = 256 / BK;
 constexpr int OPER = BM * BK;          // bytes of one operand tile per stage
 constexpr int STAGE = 2 * OPER;        // A + B
 constexpr int GROUP_M = 4;             // measured ahead of 2, 8 and 16
@@ -44,9 +47,10 @@ constexpr int ROWS_PER_LOAD = 64 / CHUNKS;          // rows one wave-load fills
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
 
-// 64-byte rows: the 16 rows one quarter-wave of an MFMA operand read touches
-// cover all 64 banks when chunk c of row r sits at slot c ^ ((r >> 2) & 3).
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & (CHUNKS - 1); }
+// The 16 rows one quarter-wave of an MFMA operand read touches cover all 64
+// banks when chunk c of row r sits at slot c ^ swz(r): (r >> 2) & 3 for
+// 64-byte rows, (r >> 1) & 7 for 128-byte rows.
+__device__ __forceinline__ int swz(int r) { return CHUNKS == 4 ? (r >> 2) & 3 : (r >> 1) & 7; }
 
 // Copies rows [r0, r0 + ROWS_PER_LOAD) x BK bytes of a K-contiguous operand
 // into LDS with one wave-wide 16-byte-per-lane direct load.
@@ -147,45 +151,50 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     };
     frags(lds, lds + OPER, 0, 0);
 
+    constexpr int SUB = BK / 32;  // MFMA k-substeps per stage (even)
+    static_assert(SUB % 2 == 0, "fragment slots alternate within a stage");
     for (int kt = 0; kt < nk; ++kt) {
         const int8_t* sa = lds + (kt % NSTAGE) * STAGE;
         const int8_t* sb = sa + OPER;
-        // -- substep 0: MFMAs on slot 0; in their shadow, the copies for stage
-        //    kt+3 (into the slot freed by iteration kt-1) and the slot-1 reads.
-        __builtin_amdgcn_sched_barrier(0);
-        issue(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
-        frags(sa, sb, 1, 1);
-        mfma_rows(0, 0, 4);
-        // 4 NJ MFMAs, 4 + NJ LDS reads, 2 LOADS_PER_WAVE copies: one read or
-        // copy after each MFMA
 #pragma unroll
-        for (int g = 0; g < 2 * NJ; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // -- substep 1, first half.
-        mfma_rows(1, 0, 2);
-        __builtin_amdgcn_sched_barrier(0);
-        // Stage kt+1 must have landed (this wave's copies: vmcnt; everyone's:
-        // the barrier); the younger stages stay in flight.  A bare s_barrier,
-        // not __syncthreads(): the latter's workgroup fence drains vmcnt to 0.
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_STAGE) : "memory");
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        // -- substep 1, second half; in its shadow, slot-0 reads of stage kt+1
-        //    (after the last stage these read a stale slot and go unused).
-        {
-            const int8_t* na = lds + ((kt + 1) % NSTAGE) * STAGE;
-            frags(na, na + OPER, 0, 0);
-        }
-        mfma_rows(1, 2, 4);
+        for (int ks = 0; ks < SUB; ++ks) {
+            const int slot = ks & 1;
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks + 1 < SUB) {
+                // MFMAs on this substep's slot; in their shadow the next
+                // substep's reads and, in the first, the copies of stage
+                // kt + NSTAGE - 1 into the slot freed by iteration kt - 1
+                if (ks == 0) issue(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
+                frags(sa, sb, ks + 1, slot ^ 1);
+                mfma_rows(slot, 0, 4);
 #pragma unroll
-        for (int g = 0; g < 2 * NJ; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int g = 0; g < 4 * NJ; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (ks == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+            } else {
+                // the last substep: half its MFMAs, then stage kt+1 must have
+                // landed (this wave's copies: vmcnt; everyone's: the barrier;
+                // a bare s_barrier, since __syncthreads()' workgroup fence
+                // drains vmcnt to 0), then its first reads beside the other half
+                // (after the last stage these read a stale slot, unused)
+                mfma_rows(slot, 0, 2);
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_STAGE) : "memory");
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                {
+                    const int8_t* na = lds + ((kt + 1) % NSTAGE) * STAGE;
+                    frags(na, na + OPER, 0, 0);
+                }
+                mfma_rows(slot, 2, 4);
+#pragma unroll
+                for (int g = 0; g < 2 * NJ; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
