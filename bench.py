@@ -396,7 +396,7 @@ def bench_sampler(ie):
 
 # ------------------------------------------------------------------ HBM traffic
 CALIB_BYTES = 1 << 30
-TRAFFIC_KERNELS = {"gemm": "gemm_i8_256_kernel", "gemv": "gemv_i8_fixed_kernel",
+TRAFFIC_KERNELS = {"gemm": "gemm_i8_256_kernel", "gemv": "gemv_i8_parted_kernel",
                    "attn": "decode_attn_balanced_kernel"}
 
 

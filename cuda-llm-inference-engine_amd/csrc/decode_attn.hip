@@ -66,22 +66,6 @@ constexpr int wave_heads() { return (D == 128 && sizeof(KV) == 4) || (D == 128 &
 template <int D, typename KV, int G>
 constexpr int wave_ring() { return D == 128 && sizeof(KV) == 4 && G < 8 ? 4 : 2; }
 
-template <typename T>
-using global_ptr = __attribute__((address_space(1))) const T*;
-
-// The same global address with its provenance hidden from alias analysis.
-// Loads through a const __restrict__ kernel argument count as invariant, and
-// the compiler sinks invariant loads past the ring's exit branches into the
-// step that consumes them, which turns the ring into issue-all-then-drain.
-// Loads through the returned pointer stay where they are written (and stay
-// global loads: the address space survives the round trip).
-template <typename T>
-__device__ __forceinline__ const T* opaque_global(const T* p) {
-    global_ptr<T> g = (global_ptr<T>)p;
-    asm volatile("" : "+s"(g));
-    return (const T*)g;
-}
-
 // Raw K/V words of one lane's d/16-element slice of one token; bf16 stays
 // packed until use so a prefetched chunk costs half the registers.
 template <int EPL, typename KV>

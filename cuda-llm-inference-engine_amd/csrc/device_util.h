@@ -159,4 +159,21 @@ __device__ __forceinline__ int32_t dot4_i8(int32_t a, int32_t b, int32_t acc) {
     return __builtin_amdgcn_sdot4(a, b, acc, false);
 }
 
+template <typename T>
+using global_ptr = __attribute__((address_space(1))) const T*;
+
+// The same global address with its provenance hidden from alias analysis.
+// Loads through a const __restrict__ kernel argument count as invariant, and
+// the compiler moves invariant loads freely (sinking them past a ring's exit
+// branches or below the MFMAs of the pass that issues them), which turns a
+// register ring into issue-all-then-drain.  Loads through the returned
+// pointer keep their place relative to memory clobbers and scheduling
+// barriers (and stay global loads: the address space survives).
+template <typename T>
+__device__ __forceinline__ const T* opaque_global(const T* p) {
+    global_ptr<T> g = (global_ptr<T>)p;
+    asm volatile("" : "+s"(g));
+    return (const T*)g;
+}
+
 }  // namespace ie

@@ -18,6 +18,12 @@
 //     rotations (no LDS round trip), then lane m of the row stores output m.
 // Requires K % 16 == 0 and 16-byte aligned A/BT; other shapes use the generic
 // kernel at the end of this file.
+//
+// Kernels by shape: gemv_i8_fixed_kernel (dot4, M <= 4, K <= 3072 and the
+// fused GPT-2 prologues), gemv_i8_mfma16_kernel (MFMA, 5 <= M <= 16,
+// K <= 4096), and at K = 8192 gemv_i8_parted_kernel (4-feature items,
+// M <= 4 or N >= 16384) and gemv_i8_slice_kernel (16-feature groups split
+// over K, the rest); gemv_i8_kernel covers any other K.
 #include <algorithm>
 
 #include "device_util.h"
@@ -333,43 +339,35 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
                          no_slot, C, GemvFusion{});
 }
 
-// 5 <= M <= 16: v_mfma_i32_16x16x64_i8 with the activations (M padded to 16
-// rows) as the A operand and 16 weight rows as the B operand.  A workgroup
-// owns 16 output features and its four waves split K four ways (so even
-// N = 768 spreads over 48 workgroups), each adding its int32 tile into LDS at
-// the end (exact).  Lane l feeds weight row n0 + l % 16, K-bytes
+// 5 <= M <= 16, K <= 4096: v_mfma_i32_16x16x64_i8 with the activations (M
+// padded to 16 rows) as the A operand and 16 weight rows as the B operand.  A
+// workgroup owns 16 output features and its four waves split K four ways (so
+// even N = 768 spreads over 48 workgroups), each adding its int32 tile into
+// LDS at the end (exact).  Lane l feeds weight row n0 + l % 16, K-bytes
 // 16 * (l / 16) .. +16 of each 64-byte K step, so one 16-byte load per lane
 // per MFMA streams 1 KiB of weights; dot4 would need 4 instructions per weight
 // byte at M = 16, which caps it below HBM speed.  Accumulator v of lane l is
-// C[4 * (l / 16) + v][n0 + l % 16].  For K <= 4096 the activation block is
-// staged in LDS (or built there by the fused prologue); beyond that each lane
-// reads its A fragment straight from global memory (the block is L2-resident).
-// Weight loads run U steps ahead of the MFMAs.  With the activations read
-// from global memory (K > 4096), NG groups of 16 output features share each
-// activation fragment: one A load feeds NG MFMAs, so the activations cost
-// 1/NG of the weights' L2 and address traffic instead of as much again.
-template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false, int NG = 1>
+// C[4 * (l / 16) + v][n0 + l % 16].  The activation block is staged in LDS
+// (or built there by the fused prologue); weight loads run U steps ahead of
+// the MFMAs.
+template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false>
 __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
     int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
     const float* residual, void* C, GemvFusion f) {
     constexpr int K = K64 * 64;
     static_assert(K64 % 4 == 0, "four waves split K");
-    constexpr int KW = K64 / 4;                // K steps per wave
-    constexpr bool A_LDS = K <= 4096;
-    static_assert(A_LDS || SRC == kSrcInt8, "fused prologues stage A in LDS");
-    static_assert(NG == 1 || (!A_LDS && EPI != kEpiQKV), "feature groups share global activations");
+    static_assert(K <= 4096, "the activation block fits LDS");
+    constexpr int KW = K64 / 4;  // K steps per wave
     // weight steps in flight per lane: the largest divisor of KW up to 8
-    // (up to 4 with several feature groups, whose loads multiply by NG)
-    constexpr int UMAX = NG > 1 ? 4 : 8;
-    constexpr int U = KW <= UMAX ? KW : KW % UMAX == 0 ? UMAX : KW % 6 == 0 && UMAX >= 6 ? 6 : KW % 4 == 0 ? 4 : 2;
+    constexpr int U = KW <= 8 ? KW : KW % 8 == 0 ? 8 : KW % 6 == 0 ? 6 : KW % 4 == 0 ? 4 : 2;
     static_assert(KW % U == 0, "whole batches");
-    __shared__ i32x4 a_lds[A_LDS ? 16 * K / 16 : 1];
+    __shared__ i32x4 a_lds[16 * K / 16];
     __shared__ float s_sa[16];
-    __shared__ i32x4 red[3][NG][64];
+    __shared__ i32x4 red[3][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, kq = lane >> 4;
-    const int n0 = blockIdx.x * 16 * NG;
+    const int n0 = blockIdx.x * 16;
     const int kb = wave * KW;  // first K step of this wave
 
     auto ldw = [&](const int8_t* p) {
@@ -380,115 +378,82 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
     };
     // Epilogue operands of this lane's outputs (rows 4 kq + v, column n0 +
     // col; only wave 0 stores) requested ahead of the weights.
-    EpiIn ein[NG][4];
+    EpiIn ein[4];
     size_t slot[16];
     if (wave == 0) {
 #pragma unroll
-        for (int g = 0; g < NG; ++g)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                ein[g][v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(n0 + 16 * g + col, N - 1), N, sB, bias,
-                                          residual);
+        for (int v = 0; v < 4; ++v)
+            ein[v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(n0 + col, N - 1), N, sB, bias, residual);
         if constexpr (EPI == kEpiQKV) qkv_slots<16>(f, M, slot);
     }
-    const int8_t* w[NG];
+    const int8_t* w = BT + (size_t)min(n0 + col, N - 1) * K + kq * 16;
+    i32x4 wv[U];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) w[g] = BT + (size_t)min(n0 + 16 * g + col, N - 1) * K + kq * 16;
-    const int8_t* arow = A + (size_t)min(col, M - 1) * K + kq * 16;  // global A (K > 4096)
-    i32x4 wv[U][NG], ag[A_LDS ? 1 : U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int g = 0; g < NG; ++g) wv[u][g] = ldw(w[g] + (size_t)(kb + u) * 64);
-        if constexpr (!A_LDS) ag[u] = *reinterpret_cast<const i32x4*>(arow + (size_t)(kb + u) * 64);
-    }
+    for (int u = 0; u < U; ++u) wv[u] = ldw(w + (size_t)(kb + u) * 64);
 
-    if constexpr (A_LDS) {
-        if constexpr (SRC == kSrcInt8) {
-            for (int i = threadIdx.x; i < 16 * (K / 16); i += 256) {
-                const int m = i / (K / 16);
-                const int mm = m < M ? m : M - 1;
-                a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)mm * K)[i - m * (K / 16)];
+    if constexpr (SRC == kSrcInt8) {
+        for (int i = threadIdx.x; i < 16 * (K / 16); i += 256) {
+            const int m = i / (K / 16);
+            const int mm = m < M ? m : M - 1;
+            a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)mm * K)[i - m * (K / 16)];
+        }
+    } else {
+        // Wave w builds rows w, w + 4, w + 8, w + 12: RB rows' loads go out
+        // together (4 at K <= 1024, 2 at larger K for registers), so the
+        // rows cost one memory round trip per batch, not one each.
+        constexpr int RB = K <= 1024 ? 4 : 2;
+#pragma unroll
+        for (int m0 = 0; m0 < 16; m0 += 4 * RB) {
+            float4 v[RB][K / 256];
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const int m = m0 + 4 * r + wave;
+                if (m < M) stage_load<K>(f.x + (size_t)m * K, v[r], lane);
             }
-        } else {
-            // Wave w builds rows w, w + 4, w + 8, w + 12: RB rows' loads go out
-            // together (4 at K <= 1024, 2 at larger K for registers), so the
-            // rows cost one memory round trip per batch, not one each.
-            constexpr int RB = K <= 1024 ? 4 : 2;
 #pragma unroll
-            for (int m0 = 0; m0 < 16; m0 += 4 * RB) {
-                float4 v[RB][K / 256];
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    const int m = m0 + 4 * r + wave;
-                    if (m < M) stage_load<K>(f.x + (size_t)m * K, v[r], lane);
-                }
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    const int m = m0 + 4 * r + wave;
-                    int32_t* dst = reinterpret_cast<int32_t*>(a_lds + m * (K / 16));
-                    if (m < M)
-                        stage_compute<K, SRC>(v[r], f, dst, &s_sa[m], lane);
-                    else
-                        zero_row<K>(dst, &s_sa[m], lane);
-                }
+            for (int r = 0; r < RB; ++r) {
+                const int m = m0 + 4 * r + wave;
+                int32_t* dst = reinterpret_cast<int32_t*>(a_lds + m * (K / 16));
+                if (m < M)
+                    stage_compute<K, SRC>(v[r], f, dst, &s_sa[m], lane);
+                else
+                    zero_row<K>(dst, &s_sa[m], lane);
             }
         }
-        __syncthreads();
     }
+    __syncthreads();
     const float* sa_src = SRC == kSrcInt8 ? sA : s_sa;
 
     // Two accumulators alternate so consecutive MFMAs do not wait on each
     // other; their integer sum is exact.
-    i32x4 acc[NG], acc1[NG];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) acc[g] = acc1[g] = i32x4{0, 0, 0, 0};
+    i32x4 acc = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
 #pragma unroll 1
     for (int k0 = 0; k0 < KW; k0 += U) {
-        i32x4 av[U], cur[U][NG];
+        i32x4 av[U], cur[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if constexpr (A_LDS)
-                av[u] = a_lds[col * (K / 16) + (kb + k0 + u) * 4 + kq];
-            else
-                av[u] = ag[u];
-#pragma unroll
-            for (int g = 0; g < NG; ++g) cur[u][g] = wv[u][g];
+            av[u] = a_lds[col * (K / 16) + (kb + k0 + u) * 4 + kq];
+            cur[u] = wv[u];
         }
-        // next batch's weights (and global A fragments) in flight during the MFMAs
+        // next batch's weights in flight during the MFMAs
         if (k0 + U < KW) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-#pragma unroll
-                for (int g = 0; g < NG; ++g) wv[u][g] = ldw(w[g] + (size_t)(kb + k0 + U + u) * 64);
-                if constexpr (!A_LDS) ag[u] = *reinterpret_cast<const i32x4*>(arow + (size_t)(kb + k0 + U + u) * 64);
-            }
+            for (int u = 0; u < U; ++u) wv[u] = ldw(w + (size_t)(kb + k0 + U + u) * 64);
         }
 #pragma unroll
-        for (int u = 0; u < U; u += 2)
-#pragma unroll
-            for (int g = 0; g < NG; ++g) {
-                acc[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u], cur[u][g], acc[g], 0, 0, 0);
-                if (u + 1 < U)
-                    acc1[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u + 1], cur[u + 1][g], acc1[g], 0, 0, 0);
-            }
+        for (int u = 0; u < U; u += 2) {
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u], cur[u], acc, 0, 0, 0);
+            if (u + 1 < U) acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[u + 1], cur[u + 1], acc1, 0, 0, 0);
+        }
     }
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        acc[g] += acc1[g];
-        if (wave > 0) red[wave - 1][g][lane] = acc[g];
-    }
+    acc += acc1;
+    if (wave > 0) red[wave - 1][lane] = acc;
     __syncthreads();
     if (wave > 0) return;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        acc[g] += red[0][g][lane];
-        acc[g] += red[1][g][lane];
-        acc[g] += red[2][g][lane];
-    }
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-    const int n = n0 + 16 * g + col;
+    acc += red[0][lane];
+    acc += red[1][lane];
+    acc += red[2][lane];
+    const int n = n0 + col;
     if (n < N) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -502,38 +467,53 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma16_kernel(
                     for (int q = 0; q < 4; ++q)
                         if (kq == q) sl = slot[4 * q + v];
                 }
-                gemv_store<EPI>(C, m, n, N, acc[g][v], sa, ein[g][v], sl, f);
+                gemv_store<EPI>(C, m, n, N, acc[v], sa, ein[v], sl, f);
             }
         }
     }
-    }
 }
 
-// K = 8192, 2 <= M <= 16: the MFMA GEMV made persistent.  One workgroup per
-// CU stages the 16 x K activation block (rows past M repeat row M - 1) in LDS
-// once, 128 KiB, and walks 16-feature groups g = blockIdx.x, + gridDim.x, ...;
-// its four waves split each group's K four ways and add their int32 tiles in
-// LDS (exact), as the per-group kernel does.  The activations cost 32 MiB of
-// L2 reads in all instead of as much as the weights, and each wave's weight
-// loads run U steps ahead across group boundaries, so the stream does not
-// drain between groups.
-template <int EPI, int K64, bool NT, int NW>
-__global__ __launch_bounds__(64 * NW) void gemv_i8_mfma16_persist_kernel(
-    int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT, const float* __restrict__ sA,
-    const float* __restrict__ sB, const float* bias, const float* residual, void* C) {
-    constexpr int K = K64 * 64;
-    constexpr int KW = K64 / NW;  // K steps per wave and group
-    constexpr int U = 8;          // weight steps in flight per lane
-    static_assert(KW % U == 0, "whole batches per group");
-    constexpr int NB = KW / U;   // batches per group
-    __shared__ i32x4 a_lds[16 * K / 16];
-    __shared__ i32x4 red[NW - 1][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// K = 8192, 2 <= M <= 16: one wave per (16-feature group, K slice).
+//
+// The weights are the only HBM stream, so the rate is set by how many of
+// their loads each CU keeps in flight.  A workgroup of 8 waves (one per CU:
+// the activation block fills its LDS) gives each wave one group's K range of
+// 8192 / KS bytes, KS = 2^ks_log slices per group chosen by the launcher so
+// that every wave of the GPU has work.  A wave streams its range through a
+// ring of R register sets of U 16-byte loads: set r is refilled right after
+// its MFMAs, so (R - 1) U loads stay in flight while one set is consumed, and
+// no register copy forces an early wait.  MFMA operands as in the kernels
+// above: lane (col, kq) supplies feature col's and activation row col's
+// K-bytes 64 s + 16 kq .. + 16 of step s.  The M activation rows sit in LDS
+// with rows padded to K + 16 bytes, so the 16 lanes reading one K chunk of 16
+// rows fall on distinct banks; rows past M read row M - 1 (results
+// discarded).  KS > 1: a group's slices are waves of one workgroup that add
+// their int32 tiles in LDS (exact), and each wave has at most one group (the
+// launcher sizes the grid so).  KS = 1: waves walk groups g, g + 8 gridDim.x,
+// ... and store each as it completes.
+template <int EPI, bool NT, int R>
+__global__ __launch_bounds__(512) void gemv_i8_slice_kernel(int M, int N, int ks_log, const int8_t* __restrict__ A,
+                                                            const int8_t* __restrict__ BT,
+                                                            const float* __restrict__ sA,
+                                                            const float* __restrict__ sB, const float* bias,
+                                                            const float* residual, void* C) {
+    constexpr int K = 8192, U = 8, LDA = K + 16;
+    constexpr int SB_LOG = 4;  // log2(128 / U)
+    __shared__ __attribute__((aligned(16))) int8_t a_lds[16 * LDA];
+    __shared__ i32x4 red[8][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    const int kb = wave * KW;
+    const int ks = 1 << ks_log;
+    const int slice = wave & (ks - 1), gslot = wave >> ks_log;
+    const int nb_log = SB_LOG - ks_log;  // batches of U steps per item: 128 / ks / U (>= R)
+    const int nb = 1 << nb_log;
     const int ngroups = (N + 15) / 16;
-    const int mine = (int)blockIdx.x < ngroups ? (ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
-    const int nbat = mine * NB;
+    const int gstride = (int)gridDim.x * (8 >> ks_log);
+    const int g0 = (int)blockIdx.x + (int)gridDim.x * gslot;
+    const int nitems = g0 < ngroups ? (ngroups - 1 - g0) / gstride + 1 : 0;
+    const int total = nitems << nb_log;  // this wave's batches
+    const int kbyte0 = slice * (K >> ks_log);
 
     auto ldw = [&](const int8_t* p) {
         if constexpr (NT)
@@ -541,75 +521,232 @@ __global__ __launch_bounds__(64 * NW) void gemv_i8_mfma16_persist_kernel(
         else
             return *reinterpret_cast<const i32x4*>(p);
     };
-    // weights of batch bi: group blockIdx.x + (bi / NB) gridDim.x, steps
-    // kb + (bi % NB) U .. + U
-    auto wrow = [&](int bi) {
-        const int g = (int)blockIdx.x + (bi / NB) * (int)gridDim.x;
-        return BT + (size_t)min(g * 16 + col, N - 1) * K + kq * 16 + (size_t)(kb + (bi % NB) * U) * 64;
+    // first weight byte of batch b: item b >> nb_log, steps (b & (nb - 1)) U ..
+    auto wptr = [&](int b) {
+        const int g = g0 + (b >> nb_log) * gstride;
+        return BT + (size_t)min(g * 16 + col, N - 1) * K + kbyte0 + (b & (nb - 1)) * (U * 64) + kq * 16;
     };
-    i32x4 wv[U];
-    if (nbat > 0) {
-        const int8_t* w = wrow(0);
+
+    // Issue order: activation rows, row scales, then the ring's first R
+    // batches; loads retire in order, so the LDS stores below wait only for
+    // the rows.
+    i32x4 stage[16];
 #pragma unroll
-        for (int u = 0; u < U; ++u) wv[u] = ldw(w + (size_t)u * 64);
+    for (int j = 0; j < 16; ++j)
+        if (j < M) stage[j] = reinterpret_cast<const i32x4*>(A + (size_t)j * K)[threadIdx.x];
+    float sa[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sa[v] = EPI != IE_EPI_I32 ? sA[min(4 * kq + v, M - 1)] : 0.0f;
+    // (unconditional: a wave without a group loads valid rows it never uses,
+    // and the compiler can count every set as issued)
+    i32x4 w[R][U];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int8_t* p = wptr(r);
+#pragma unroll
+        for (int u = 0; u < U; ++u) w[r][u] = ldw(p + u * 64);
     }
-    for (int i = threadIdx.x; i < 16 * (K / 16); i += 64 * NW) {
-        const int m = i / (K / 16);
-        a_lds[i] = reinterpret_cast<const i32x4*>(A + (size_t)min(m, M - 1) * K)[i - m * (K / 16)];
-    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if (j < M) reinterpret_cast<i32x4*>(a_lds + j * LDA)[threadIdx.x] = stage[j];
     __syncthreads();
 
-    i32x4 acc = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
-    EpiIn ein[4];
-#pragma unroll 1
-    for (int bi = 0; bi < nbat; ++bi) {
-        const int g = (int)blockIdx.x + (bi / NB) * (int)gridDim.x;
-        if (bi % NB == 0 && wave == 0) {
-            // the group's epilogue operands, requested with its first weights
+    auto finish = [&](int g, const i32x4& acc) {
+        const int n = g * 16 + col;
+        EpiIn e[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) e[v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(n, N - 1), N, sB, bias, residual);
+        if (n < N) {
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-                ein[v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(g * 16 + col, N - 1), N, sB, bias, residual);
+                if (4 * kq + v < M) gemv_store<EPI>(C, 4 * kq + v, n, N, acc[v], sa[v], e[v], 0, GemvFusion{});
         }
-        i32x4 cur[U];
+    };
+
+    // Two accumulators alternate so consecutive MFMAs do not wait on each
+    // other; their integer sum is exact.
+    i32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    const int8_t* arow = a_lds + min(col, M - 1) * LDA + kbyte0 + kq * 16;
+    // One pass over the R sets: MFMAs on set r (batch b + r), then, if REFILL,
+    // set r reloaded with batch b + r + R.  total is a multiple of R (ks <= 4),
+    // so every body but the last refills all its sets, and the waits count
+    // the R - 1 sets issued after each one.
+    auto body = [&](int b, auto refill) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) cur[u] = wv[u];
-        if (bi + 1 < nbat) {  // next batch, possibly the next group's, in flight
-            const int8_t* w = wrow(bi + 1);
+        for (int r = 0; r < R; ++r) {
+            const int bi = b + r;
+            const int8_t* ap = arow + (bi & (nb - 1)) * (U * 64);
 #pragma unroll
-            for (int u = 0; u < U; ++u) wv[u] = ldw(w + (size_t)u * 64);
-        }
-        const int kk = kb + (bi % NB) * U;
-#pragma unroll
-        for (int u = 0; u < U; u += 2) {
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_lds[col * (K / 16) + (kk + u) * 4 + kq], cur[u], acc, 0,
-                                                        0, 0);
-            acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_lds[col * (K / 16) + (kk + u + 1) * 4 + kq], cur[u + 1],
-                                                         acc1, 0, 0, 0);
-        }
-        if (bi % NB == NB - 1) {  // group done (uniform across the workgroup)
-            acc += acc1;
-            if (wave > 0) red[wave - 1][lane] = acc;
-            __syncthreads();
-            if (wave == 0) {
-#pragma unroll
-                for (int w = 0; w < NW - 1; ++w) acc += red[w][lane];
-                const int n = g * 16 + col;
-                if (n < N) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int m = 4 * kq + v;
-                        if (m < M) {
-                            float sa = 0.0f;
-                            if constexpr (EPI != IE_EPI_I32) sa = sA[m];
-                            gemv_store<EPI>(C, m, n, N, acc[v], sa, ein[v], 0, GemvFusion{});
-                        }
-                    }
-                }
+            for (int u = 0; u < U; u += 2) {
+                acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const i32x4*>(ap + u * 64), w[r][u],
+                                                             acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const i32x4*>(ap + (u + 1) * 64),
+                                                             w[r][u + 1], acc1, 0, 0, 0);
             }
-            __syncthreads();  // red is rewritten by the next group
-            acc = i32x4{0, 0, 0, 0};
-            acc1 = i32x4{0, 0, 0, 0};
+            if constexpr (decltype(refill)::value) {
+                const int8_t* p = wptr(bi + R);
+#pragma unroll
+                for (int u = 0; u < U; ++u) w[r][u] = ldw(p + u * 64);
+            }
+            if (ks_log == 0 && (bi & (nb - 1)) == nb - 1) {
+                finish(g0 + (bi >> nb_log) * gstride, acc0 + acc1);
+                acc0 = acc1 = i32x4{0, 0, 0, 0};
+            }
         }
+    };
+    int b = 0;
+#pragma unroll 1
+    for (; b + R < total; b += R) body(b, std::true_type{});
+    if (total > 0) body(b, std::false_type{});
+    if (ks_log > 0) {
+        acc0 += acc1;
+        if (slice > 0 && nitems > 0) red[wave][lane] = acc0;
+        __syncthreads();
+        if (slice == 0 && nitems > 0) {
+            for (int t = 1; t < ks; ++t) acc0 += red[wave + t][lane];
+            finish(g0, acc0);
+        }
+    }
+}
+
+// K = 8192, M <= 4 MB: the MFMA GEMV over 4-feature items, K in four parts.
+//
+// The weight stream runs fastest when each load instruction reads a few rows
+// with long runs, one row set finished before the next starts (4 rows x 256
+// bytes per wave instruction, walked row set by row set, streams about 15%
+// faster than the 16 rows x 64 bytes of a 16-feature MFMA fragment).  So here
+// the 16 columns of v_mfma_i32_16x16x64_i8 are 4 features x 4 K-parts and its
+// 16 rows are 4 activation rows x the same 4 parts: column c is feature c / 4,
+// part c % 4 (row r likewise), and at step s (256 K-bytes) lane (c, q)
+// supplies bytes 256 s + 16 (4 q + c % 4) .. + 16 of its feature (B) and of
+// its activation row (A).  Row r and column c pair equal K positions exactly
+// when r % 4 == c % 4; those entries hold each part's int32 sum, the rest are
+// discarded, and the four parts (the four lanes of a quad) are added with
+// DPP at the end (exact).  A wave instruction loads 4 rows x 256 contiguous
+// bytes, 64 contiguous bytes per lane quad.  MB blocks of 4 activation rows
+// each take one MFMA per weight fragment.
+//
+// One item = 4 features x all of K = 32 steps = R (4) batches of U (8)
+// loads: one pass over the register ring.  Waves walk items b + gridDim.x w,
+// + 8 gridDim.x, ...; each pass refills the ring with the next item's
+// weights, so the stream does not drain between items, and requests the next
+// item's epilogue operands after storing the current one's, so no wait
+// covers more than the loads issued before it.
+template <int EPI, bool NT, int MB>
+__global__ __launch_bounds__(512) void gemv_i8_parted_kernel(int M, int N, const int8_t* __restrict__ A,
+                                                             const int8_t* __restrict__ BT,
+                                                             const float* __restrict__ sA,
+                                                             const float* __restrict__ sB, const float* bias,
+                                                             const float* residual, void* C) {
+    // LDS rows padded to K + 64 bytes: the 16 lanes reading one step's
+    // fragments (4 rows x 4 parts) fall on distinct banks.
+    constexpr int K = 8192, U = 8, R = 4, LDA = K + 64;
+    static_assert(R * U * 256 == K, "one item per ring pass");
+    __shared__ __attribute__((aligned(16))) int8_t a_lds[4 * MB * LDA];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, q = lane >> 4;
+    const int part = col & 3, f = col >> 2;
+    const int nitems_all = (N + 3) / 4;
+    const int stride = (int)gridDim.x * 8;
+    const int i0 = (int)blockIdx.x + (int)gridDim.x * wave;
+    const int nitems = i0 < nitems_all ? (nitems_all - 1 - i0) / stride + 1 : 0;
+
+    auto ldw = [&](const int8_t* p) {
+        if constexpr (NT)
+            return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+        else
+            return *reinterpret_cast<const i32x4*>(p);
+    };
+    const int kofs = (4 * q + part) * 16;  // this lane's 16 bytes within a step
+    const int8_t* bt = opaque_global(BT);
+    auto wrow = [&](int t) {  // feature f of the wave's item t
+        return bt + (size_t)min(4 * (i0 + t * stride) + f, N - 1) * K + kofs;
+    };
+    // The lane's output of an item: block part (when part < MB), row
+    // 4 part + q of C, feature f; the epilogue operands are read clamped.
+    const int out_m = 4 * part + q;
+    const bool out_ok = part < MB && out_m < M;
+    const int m_c = min(out_m, M - 1);
+    auto out_n = [&](int t) { return 4 * (i0 + t * stride) + f; };
+
+    // Issue order: activation rows, the first item's weights, its epilogue
+    // operands; the LDS stores wait only for the rows.
+    i32x4 stage[4 * MB];
+#pragma unroll
+    for (int j = 0; j < 4 * MB; ++j)
+        if (j < M) stage[j] = reinterpret_cast<const i32x4*>(A + (size_t)j * K)[threadIdx.x];
+    i32x4 w[R][U];
+    {
+        const int8_t* p = wrow(0);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int u = 0; u < U; ++u) w[r][u] = ldw(p + (r * U + u) * 256);
+    }
+    const float sa = EPI != IE_EPI_I32 ? sA[m_c] : 0.0f;
+    EpiIn e = epi_load<EPI>(m_c, min(out_n(0), N - 1), N, sB, bias, residual);
+#pragma unroll
+    for (int j = 0; j < 4 * MB; ++j)
+        if (j < M) reinterpret_cast<i32x4*>(a_lds + j * LDA)[threadIdx.x] = stage[j];
+    __syncthreads();
+
+    // A operand of block j: activation row 4 j + f (clamped to M - 1; those
+    // rows' results are never stored), the same 16 bytes as B.
+    const int8_t* arow[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) arow[j] = a_lds + min(4 * j + f, M - 1) * LDA + kofs;
+
+    auto pass = [&](int t, auto refill) {
+        i32x4 acc[MB][2];
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[j][0] = acc[j][1] = i32x4{0, 0, 0, 0};
+        const int8_t* pn = wrow(t + 1);
+        // The activation fragments are the same for every item; an opaque
+        // zero offset keeps the compiler from hoisting all 32 of them into
+        // registers, where they would crowd out the ring.
+        int aofs = 0;
+        asm volatile("" : "+v"(aofs));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s = r * U + u;
+#pragma unroll
+                for (int j = 0; j < MB; ++j)
+                    acc[j][u & 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        *reinterpret_cast<const i32x4*>(arow[j] + aofs + s * 256), w[r][u], acc[j][u & 1], 0, 0, 0);
+            }
+            if constexpr (decltype(refill)::value) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) w[r][u] = ldw(pn + (r * U + u) * 256);
+            }
+            // keep each set's refill right behind its MFMAs (the compiler
+            // would otherwise sink all refills to the end of the pass)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // acc[j][.][v] of lane (c, q) is row 4 q + v of block j: part v of
+        // activation row 4 j + q.  Keep v = c % 4 (the matching part), add
+        // the quad's four parts; then lane (part, f, q) takes block part.
+        int32_t mine = 0;
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            const i32x4 x4 = acc[j][0] + acc[j][1];
+            int32_t x = part == 0 ? x4[0] : part == 1 ? x4[1] : part == 2 ? x4[2] : x4[3];
+            x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xf, 0xf, false);  // quad_perm [1, 0, 3, 2]
+            x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xf, 0xf, false);  // quad_perm [2, 3, 0, 1]
+            mine = part == j ? x : mine;
+        }
+        const int n = out_n(t);
+        if (out_ok && n < N) gemv_store<EPI>(C, out_m, n, N, mine, sa, e, 0, GemvFusion{});
+        if constexpr (decltype(refill)::value) e = epi_load<EPI>(m_c, min(out_n(t + 1), N - 1), N, sB, bias, residual);
+    };
+    if (nitems > 0) {
+        int t = 0;
+#pragma unroll 1
+        for (; t + 1 < nitems; ++t) pass(t, std::true_type{});
+        pass(t, std::false_type{});
     }
 }
 
@@ -661,24 +798,47 @@ void launch_fixed(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFu
             a.M, a.N, a.A, a.BT, a.sA, a.sB, a.bias, a.residual, a.C, f);
 }
 
-template <int EPI, int K64, int SRC = kSrcInt8, int NG = 1>
+template <int EPI, int K64, int SRC = kSrcInt8>
 void launch_mfma16(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFusion{}) {
-    const unsigned blocks = (unsigned)((a.N + 16 * NG - 1) / (16 * NG));
+    const unsigned blocks = (unsigned)((a.N + 15) / 16);
     const bool nt = (size_t)a.N * K64 * 64 >= kStreamWeightBytes;
-    auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true, NG> : gemv_i8_mfma16_kernel<EPI, K64, SRC, false, NG>;
+    auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true> : gemv_i8_mfma16_kernel<EPI, K64, SRC, false>;
     k<<<blocks, 256, 0, s>>>(a.M, a.N, reinterpret_cast<const int8_t*>(a.A),
                              reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual,
                              a.C, f);
 }
 
-template <int EPI, int K64>
-void launch_mfma16_persist(const GemmArgs& a, hipStream_t s) {
-    constexpr int NW = 8;  // 8 waves split each group's K: measured ahead of 4 and 16
-    const unsigned blocks = (unsigned)std::min((a.N + 15) / 16, num_cus());
-    const bool nt = (size_t)a.N * K64 * 64 >= kStreamWeightBytes;
-    auto* k = nt ? gemv_i8_mfma16_persist_kernel<EPI, K64, true, NW> : gemv_i8_mfma16_persist_kernel<EPI, K64, false, NW>;
-    k<<<blocks, 64 * NW, 0, s>>>(a.M, a.N, reinterpret_cast<const int8_t*>(a.A),
-                                         reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
+template <int EPI>
+void launch_slice(const GemmArgs& a, hipStream_t s) {
+    const int groups = (a.N + 15) / 16;
+    const int cus = num_cus();
+    // K slices per group: the most that still give every wave at most one
+    // group (groups x KS <= 8 waves x CUs), up to 4 (the kernel's ring needs
+    // a multiple of R = 4 batches per wave).
+    int ks_log = 0;
+    while (ks_log < 2 && (long long)groups * (2 << ks_log) <= 8LL * cus) ++ks_log;
+    const unsigned blocks = ks_log == 0 ? (unsigned)std::min(groups, cus) : (unsigned)((groups << ks_log) + 7) / 8;
+    const bool nt = (size_t)a.N * 8192 >= kStreamWeightBytes;
+    // a ring of 2 sets of 8 loads: measured level with 4 sets
+    auto* k = nt ? gemv_i8_slice_kernel<EPI, true, 2> : gemv_i8_slice_kernel<EPI, false, 2>;
+    k<<<blocks, 512, 0, s>>>(a.M, a.N, ks_log, reinterpret_cast<const int8_t*>(a.A),
+                             reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
+}
+
+template <int EPI>
+void launch_parted(const GemmArgs& a, hipStream_t s) {
+    const int items = (a.N + 3) / 4;
+    const unsigned blocks = (unsigned)std::min(items, num_cus());
+    const bool nt = (size_t)a.N * 8192 >= kStreamWeightBytes;
+    auto go = [&](auto mb) {
+        constexpr int MB = decltype(mb)::value;
+        auto* k = nt ? gemv_i8_parted_kernel<EPI, true, MB> : gemv_i8_parted_kernel<EPI, false, MB>;
+        k<<<blocks, 512, 0, s>>>(a.M, a.N, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
+                                 a.sA, a.sB, a.bias, a.residual, a.C);
+    };
+    if (a.M <= 4) go(std::integral_constant<int, 1>{});
+    else if (a.M <= 8) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 4>{});
 }
 
 template <int EPI, int K, int SRC>
@@ -695,21 +855,16 @@ void launch_mt(const GemmArgs& a, hipStream_t s) {
         if (a.K == 768) return launch_mfma16<EPI, 12>(a, s);
         if (a.K == 3072) return launch_mfma16<EPI, 48>(a, s);
     }
-    // K = 8192: one row streams best with dot4; from two rows on, the dot4
-    // work per pass (no cross-pass prefetch at this K) outlasts the loads, so
-    // the MFMA kernel takes over.
+    // K = 8192 (measured at N = 8192 and 28672, M = 1..16, fraction of HBM
+    // peak on one box): the 4-feature-item kernel for M <= 4 (N = 28672:
+    // M = 1 0.76 -> 0.79 against dot4, M = 4 0.62 -> 0.79 against the 16-row
+    // MFMA kernels) and for any M once each wave has two items or more
+    // (N >= 16384; N = 28672, M = 16: 0.64 -> 0.69); below that the K-sliced
+    // 16-feature kernel, whose activation staging costs a quarter as much
+    // per wave (N = 8192, M = 16: 0.55 against 0.49).
     if (a.K == 8192) {
-        if constexpr (MT == 1) {
-            return launch_fixed<1, EPI, 512>(a, s);
-        } else {
-            // Measured at N = 8192 and 28672, M = 2..16 (fraction of HBM peak):
-            // many groups and M >= 5, the persistent kernel (N = 28672, M = 16:
-            // 0.48 -> 0.60); around N = 8192, two feature groups per workgroup
-            // (M = 16: 0.41 -> 0.49, M = 2: 0.53 -> 0.57); otherwise one.
-            if (a.N >= 16384 && a.M >= 5) return launch_mfma16_persist<EPI, 128>(a, s);
-            if (a.N >= 8192 && a.N < 16384) return launch_mfma16<EPI, 128, kSrcInt8, 2>(a, s);
-            return launch_mfma16<EPI, 128>(a, s);
-        }
+        if (a.M <= 4 || a.N >= 16384) return launch_parted<EPI>(a, s);
+        return launch_slice<EPI>(a, s);
     }
     // Specialised K: the GPT-2 widths.
     if constexpr (MT <= 4) {

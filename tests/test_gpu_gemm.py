@@ -98,17 +98,19 @@ def test_i32_odd_shapes(ie, orc, M, N, K, path):
 
 
 @pytest.mark.parametrize("M,N", [(2, 8200), (7, 8200), (16, 8192), (8, 4096), (4, 28672), (5, 16400),
-                                 (13, 16400), (16, 28672)])
+                                 (13, 16400), (16, 28672), (1, 8193), (2, 8194), (3, 8195), (6, 4099),
+                                 (11, 1027), (16, 30), (9, 5), (4, 1)])
 def test_i32_gemv_k8192_paths(ie, orc, M, N):
-    """K = 8192 decode GEMV dispatch: one or two 16-feature groups per workgroup
-    (N below 16384) and the persistent kernel (N >= 16384, M >= 5), with partial
-    last groups (N % 16 != 0 only for N = 8200, 16400) and M not a multiple of 4."""
+    """K = 8192 decode GEMV: every block count of activation rows (M 1-4, 5-8,
+    9-16), one to four 4-feature items per wave (N = 28672), a partial last
+    item (N % 4 != 0) and fewer items than waves (N = 1 .. 30)."""
     i32_case(ie, orc, M, N, 8192, ie.PATH_GEMV, M * 3 + N)
 
 
+@pytest.mark.parametrize("M,N", [(13, 16400), (3, 8195), (6, 4099)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
-def test_persistent_gemv_epilogues(ie, orc, epi):
-    M, N, K = 13, 16400, 8192
+def test_k8192_gemv_epilogues(ie, orc, epi, M, N):
+    K = 8192
     A, W = problem(M, N, K, 77 + epi)
     r = rng(6 + epi)
     bias = (r.standard_normal(N) * 0.5).astype(np.float32)
