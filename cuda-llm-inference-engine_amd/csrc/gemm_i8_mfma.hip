@@ -167,12 +167,12 @@ void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s) {
         launch_gemm_i8_big(a, s);
         return;
     }
-    // Prefill-sized M with wide N (a batch of prompts through the QKV and
-    // FFN-up projections): the 128x128 LDS tile beats per-wave streaming
-    // (M=2048: 22.3 vs 29.4 us at N=2304, 31.4 vs 38.7 us at N=3072); at
-    // N=768 or M=512 streaming stays ahead.
-    if (a.M >= 1024 && a.N >= 2048) {
-        dispatch_epilogue<MfmaLaunch>(a.epi, a, s);
+    // Prefill-sized problems: the multi-stage LDS tile kernel (M = 2048:
+    // 22.1 -> 12.1 us at N = 2304, 37.7 -> 13.0 us at K = 3072, N = 768;
+    // at par with or ahead of hipBLASLt on the same shapes); below 64 tiles,
+    // register streaming.
+    if (gemm_i8_tile_applies(a)) {
+        launch_gemm_i8_tile(a, s);
         return;
     }
     if (gemm_i8_stream_applies(a)) {

@@ -200,65 +200,53 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 
-    // Epilogue.  All 64 row scales and 4 column scales of this lane are
-    // gathered before the first store, so their latency is paid once, not once
-    // per store.  Lane l of a 32x32 block holds rows 8q + 4(l/32) + r (q, r < 4)
-    // of column l % 32.
+    // Epilogue.  Lane l of a 32x32 block holds rows 8q + 4(l/32) + r (q, r < 4)
+    // of column l % 32.  Every operand the stores of a 32-row block need
+    // (scales, bias, residual; clamped indices) is gathered before its first
+    // store and consumed once in straight-line code: loaded inside the branchy
+    // store loop, each would wait for all earlier stores (vmcnt counts stores,
+    // and C may alias them).  Two waves per SIMD leave no room for all 64 row
+    // scales beside the accumulators, so they are gathered one block at a time.
     const int h = lane >> 5;
     const int rbase = m0 + wm * 128 + 4 * h;
     const int cbase = n0 + wn * 32 * NJ + (lane & 31);
-    if constexpr (NW == 8 && EPI != IE_EPI_I32) {
-        // two waves per SIMD leave no room for all 64 row scales beside the
-        // accumulators: gather them one 32-row block at a time
-        float sb[NJ];
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) sb[j] = sB[min(cbase + j * 32, N - 1)];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float sa[16];
-#pragma unroll
-            for (int v = 0; v < 16; ++v) sa[v] = sA[min(rbase + i * 32 + 8 * (v >> 2) + (v & 3), M - 1)];
-#pragma unroll
-            for (int v = 0; v < 16; ++v) asm volatile("" ::"v"(sa[v]));
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) asm volatile("" ::"v"(sb[j]));
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
-                if (m >= M) continue;
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    const int n = cbase + j * 32;
-                    if (n < N)
-                        store_epilogue<EPI, true>(C, (size_t)m * N + n, acc[i][j][v], sa[v], sb[j], bias, residual,
-                                                  n);
-                }
-            }
-        }
-        return;
-    }
-    float sa[4][16], sb[NJ];
+    constexpr bool HAS_BIAS = EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL;
+    constexpr bool HAS_RES = EPI == IE_EPI_BIAS_RESIDUAL;
+    float sb[NJ] = {}, bv[NJ] = {};
     if constexpr (EPI != IE_EPI_I32) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                sa[i][v] = sA[min(rbase + i * 32 + 8 * (v >> 2) + (v & 3), M - 1)];
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) sb[j] = sB[min(cbase + j * 32, N - 1)];
-        // Consume every scale once in straight-line code: the compiler waits
-        // for the loads here, once.  Otherwise the branchy store loop below gets
-        // a conservative vmcnt(0) before each store, and since vmcnt also counts
-        // stores, every store would wait for the previous one to retire.
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) asm volatile("" ::"v"(sa[i][v]));
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) asm volatile("" ::"v"(sb[j]));
+        for (int j = 0; j < NJ; ++j) {
+            const int n = min(cbase + j * 32, N - 1);
+            sb[j] = sB[n];
+            if constexpr (HAS_BIAS) bv[j] = bias[n];
+        }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+        float sa[16] = {}, rv[16][NJ] = {};
+        if constexpr (EPI != IE_EPI_I32) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = min(rbase + i * 32 + 8 * (v >> 2) + (v & 3), M - 1);
+                sa[v] = sA[m];
+                if constexpr (HAS_RES) {
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) rv[v][j] = residual[(size_t)m * N + min(cbase + j * 32, N - 1)];
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                asm volatile("" ::"v"(sa[v]));
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    if constexpr (HAS_RES) asm volatile("" ::"v"(rv[v][j]));
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                asm volatile("" ::"v"(sb[j]));
+                if constexpr (HAS_BIAS) asm volatile("" ::"v"(bv[j]));
+            }
+        }
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int m = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
@@ -267,8 +255,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
             for (int j = 0; j < NJ; ++j) {
                 const int n = cbase + j * 32;
                 if (n < N)
-                    store_epilogue<EPI, true>(C, (size_t)m * N + n, acc[i][j][v], sa[i][v], sb[j], bias,
-                                        residual, n);
+                    store_epilogue_v<EPI, true>(C, (size_t)m * N + n, acc[i][j][v], sa[v], sb[j], bv[j], rv[v][j]);
             }
         }
     }

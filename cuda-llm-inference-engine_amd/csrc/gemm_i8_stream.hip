@@ -119,22 +119,52 @@ __global__ __launch_bounds__(64 * KS) void gemm_i8_stream_kernel(
             for (int j = 0; j < NB; ++j) acc[j] += red[w][j][lane];
     }
 
+    // Every operand the stores need (scales, bias, residual; clamped
+    // indices) is gathered first and consumed once in straight-line code:
+    // loaded inside the branchy store loop, each would wait for all earlier
+    // stores (vmcnt counts stores, and C may alias them).
     const int cbase = n0 + r;
     const int rbase = m0 + 4 * h;
+    constexpr bool HAS_BIAS = EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL;
+    constexpr bool HAS_RES = EPI == IE_EPI_BIAS_RESIDUAL;
+    float sa[16] = {}, sb[NB] = {}, bv[NB] = {}, rv[16][NB] = {};
+    if constexpr (EPI != IE_EPI_I32) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int n = min(cbase + 32 * j, N - 1);
+            sb[j] = sB[n];
+            if constexpr (HAS_BIAS) bv[j] = bias[n];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int m = min(rbase + 8 * (v >> 2) + (v & 3), M - 1);
+            sa[v] = sA[m];
+            if constexpr (HAS_RES) {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) rv[v][j] = residual[(size_t)m * N + min(cbase + 32 * j, N - 1)];
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            asm volatile("" ::"v"(sa[v]));
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                if constexpr (HAS_RES) asm volatile("" ::"v"(rv[v][j]));
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            asm volatile("" ::"v"(sb[j]));
+            if constexpr (HAS_BIAS) asm volatile("" ::"v"(bv[j]));
+        }
+    }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
         const int n = cbase + 32 * j;
         if (n >= N) continue;
-        float sb = 0.0f;
-        if constexpr (EPI != IE_EPI_I32) sb = sB[n];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int m = rbase + 8 * (v >> 2) + (v & 3);
-            if (m < M) {
-                float sa = 0.0f;
-                if constexpr (EPI != IE_EPI_I32) sa = sA[m];
-                store_epilogue<EPI>(C, (size_t)m * N + n, acc[j][v], sa, sb, bias, residual, n);
-            }
+            if (m < M) store_epilogue_v<EPI>(C, (size_t)m * N + n, acc[j][v], sa[v], sb[j], bv[j], rv[v][j]);
         }
     }
 }

@@ -69,6 +69,11 @@ void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s);
 // 256x256-tile MFMA GEMM for large M, N (gemm_i8_mfma256.hip).
 bool gemm_i8_big_applies(const GemmArgs& a);
 void launch_gemm_i8_big(const GemmArgs& a, hipStream_t s);
+// LDS-tiled MFMA GEMM for prefill-sized problems (gemm_i8_tile.hip): tile
+// shape BM * 1000 + BN chosen for a problem, applicability, launch.
+int gemm_i8_tile_shape(const GemmArgs& a);
+bool gemm_i8_tile_applies(const GemmArgs& a);
+void launch_gemm_i8_tile(const GemmArgs& a, hipStream_t s);
 // Register-streamed MFMA GEMM for mid-size problems (gemm_i8_stream.hip).
 bool gemm_i8_stream_applies(const GemmArgs& a);
 void launch_gemm_i8_stream(const GemmArgs& a, hipStream_t s);

@@ -150,11 +150,12 @@ def test_epilogues(ie, orc, M, K, N, path, epi):
                                    (128, 768, 3072), (97, 700, 640), (130, 770, 2048)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
 def test_register_streamed_kernel(ie, orc, M, N, K, epi):
-    """Mid-size shapes (K % 128 == 0, too few 256x256 tiles for the LDS-tiled
-    kernel) run on the register-streamed MFMA kernel: ragged M and N, one and
-    two 32-column blocks per wave, K split over 4 waves (128x768x3072,
-    130x770x2048) and 2 waves (97x700x640), every epilogue; int32 and
-    Plain/Bias/Residual bit-exact, GELU to 2e-6."""
+    """Mid-size shapes (K % 128 == 0, too few 256x256 tiles for the large-tile
+    kernel): below 64 tiles of 64x64 the register-streamed MFMA kernel, with K
+    split over 4 waves (128x768x3072, 130x770x2048) and 2 waves (97x700x640);
+    above, the 64x64 LDS tile kernel (520x4100x256, 1000x2100x768).  Ragged M
+    and N, every epilogue; int32 and Plain/Bias/Residual bit-exact, GELU to
+    2e-6."""
     A, W = problem(M, N, K, 7 * M + N + K + epi)
     r = rng(11 + epi)
     bias = (r.standard_normal(N) * 0.5).astype(np.float32)
@@ -177,9 +178,10 @@ def test_register_streamed_kernel(ie, orc, M, N, K, epi):
 @pytest.mark.parametrize("M,N,K", [(1100, 2100, 768), (2048, 2304, 768)])
 @pytest.mark.parametrize("epi", [0, 2, 3, 4])
 def test_prefill_sized_wide_gemm(ie, orc, M, N, K, epi):
-    """M >= 1024 with N >= 2048 (a batch of prompts through the QKV / FFN-up
-    projections) runs on the 128x128 LDS tile: ragged M and N, int32 and
-    Plain/Residual bit-exact, GELU to 2e-6."""
+    """A batch of prompts through the QKV / FFN-up projections: the LDS tile
+    kernel with 128x64 tiles (2048x2304, two per CU) and 64x64 tiles
+    (1100x2100), two-stage ring; ragged M and N, int32 and Plain/Residual
+    bit-exact, GELU to 2e-6."""
     A, W = problem(M, N, K, 3 * M + N + epi)
     r = rng(17 + epi)
     bias = (r.standard_normal(N) * 0.5).astype(np.float32)
@@ -197,6 +199,36 @@ def test_prefill_sized_wide_gemm(ie, orc, M, N, K, epi):
         assert np.allclose(got, want, rtol=2e-6, atol=1e-7), np.abs(got - want).max()
     else:
         assert np.array_equal(got, want), np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("M,N,K", [(2100, 2200, 2048), (2048, 768, 3072), (700, 3000, 4096)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
+def test_tile_kernel_long_k(ie, orc, M, N, K, epi):
+    """The LDS tile kernel's four-stage ring (K >= 2048) with 128x64 tiles
+    (2100x2200x2048) and 64x64 tiles (the FFN-down shape 2048x768x3072,
+    700x3000x4096): ragged M and N, every epilogue, on rows around tile edges
+    (int32 also through a full column checksum); bit-exact, GELU to 2e-6."""
+    A, W = problem(M, N, K, 5 * M + N + K + epi)
+    r = rng(23 + epi)
+    bias = (r.standard_normal(N) * 0.5).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    rows = sorted({0, 1, 63, 64, 127, 128, M // 2, M - 65, M - 2, M - 1})
+    if epi == 4:
+        got = host(ie.int8_gemm(dev(Ap), dev(Wp), epilogue=ie.EPI_I32, path=ie.PATH_MFMA))
+        assert np.array_equal(got[rows], orc.gemm_i32(Ap[rows], Wp))
+        a8 = Ap.view(np.int8).reshape(M, K).astype(np.int64)
+        w8 = Wp.view(np.int8).reshape(N, K).astype(np.int64)
+        assert np.array_equal(got.astype(np.int64).sum(0), w8 @ a8.sum(0))
+        return
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi, dev(bias) if epi else None,
+                            dev(res) if epi == 3 else None, path=ie.PATH_MFMA))
+    want = orc.gemm(Ap[rows], Wp, sA[rows], sW, epi, bias if epi else None, res[rows] if epi == 3 else None)
+    if epi == 2:
+        assert np.allclose(got[rows], want, rtol=2e-6, atol=1e-7), np.abs(got[rows] - want).max()
+    else:
+        assert np.array_equal(got[rows], want), np.abs(got[rows] - want).max()
 
 
 @pytest.mark.parametrize("path", [1, 2])
