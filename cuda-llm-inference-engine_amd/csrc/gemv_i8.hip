@@ -21,9 +21,10 @@
 //
 // Kernels by shape: gemv_i8_fixed_kernel (dot4, M <= 4, K <= 3072 and the
 // fused GPT-2 prologues), gemv_i8_mfma16_kernel (MFMA, 5 <= M <= 16,
-// K <= 4096), and at K = 8192 gemv_i8_parted_kernel (4-feature items,
-// M <= 4 or N >= 16384) and gemv_i8_slice_kernel (16-feature groups split
-// over K, the rest); gemv_i8_kernel covers any other K.
+// K <= 4096), gemv_i8_burst_kernel (K = 768 / 3072 with N >= 16384 and
+// M <= 8: the LM head), and at K = 8192 gemv_i8_parted_kernel (4-feature
+// items, M <= 4 or N >= 16384) and gemv_i8_slice_kernel (16-feature groups
+// split over K, the rest); gemv_i8_kernel covers any other K.
 #include <algorithm>
 
 #include "device_util.h"
@@ -750,6 +751,102 @@ __global__ __launch_bounds__(512) void gemv_i8_parted_kernel(int M, int N, const
     }
 }
 
+// K = 256 S <= 3072 (the GPT-2 widths), M <= 4 MB: the 4-feature-item MFMA
+// GEMV above without a ring.  An item is only S load steps, so each wave
+// takes IPW consecutive items (4 IPW rows, one contiguous run of weights),
+// issues all their loads and epilogue operands at once, then computes item by
+// item; the workgroups are small (4 waves, M x K bytes of LDS) and all
+// resident at once, so a GEMV of any width is one memory round trip plus its
+// transfer (the 768 x 50257 LM head: 38.6 MB in flight together).
+template <int EPI, bool NT, int MB, int S, int IPW>
+__global__ __launch_bounds__(256) void gemv_i8_burst_kernel(int M, int N, const int8_t* __restrict__ A,
+                                                            const int8_t* __restrict__ BT,
+                                                            const float* __restrict__ sA,
+                                                            const float* __restrict__ sB, const float* bias,
+                                                            const float* residual, void* C) {
+    constexpr int K = 256 * S, LDA = K + 64;  // padded rows: conflict-free reads
+    constexpr int CH = 4 * MB * (K / 16);      // 16-byte chunks of the activation block
+    __shared__ __attribute__((aligned(16))) int8_t a_lds[4 * MB * LDA];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, q = lane >> 4;
+    const int part = col & 3, f = col >> 2;
+    const int nitems_all = (N + 3) / 4;
+    const int i0 = ((int)blockIdx.x * 4 + wave) * IPW;
+    const int kofs = (4 * q + part) * 16;
+    const int out_m = 4 * part + q;
+    const bool out_ok = part < MB && out_m < M;
+    const int m_c = min(out_m, M - 1);
+
+    auto ldw = [&](const int8_t* p) {
+        if constexpr (NT)
+            return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+        else
+            return *reinterpret_cast<const i32x4*>(p);
+    };
+    // Issue order: activation rows (rows past M repeat row M - 1), every
+    // item's weights (rows past N repeat row N - 1), epilogue operands.
+    constexpr int SPT = (CH + 255) / 256;  // staging chunks per thread
+    i32x4 stage[SPT];
+#pragma unroll
+    for (int c = 0; c < SPT; ++c) {
+        const int ch = threadIdx.x + 256 * c;
+        if (CH % 256 == 0 || ch < CH) {
+            const int r = ch / (K / 16);
+            stage[c] = reinterpret_cast<const i32x4*>(A + (size_t)min(r, M - 1) * K)[ch - r * (K / 16)];
+        }
+    }
+    i32x4 w[IPW][S];
+#pragma unroll
+    for (int it = 0; it < IPW; ++it) {
+        const int8_t* p = BT + (size_t)min(4 * (i0 + it) + f, N - 1) * K + kofs;
+#pragma unroll
+        for (int s = 0; s < S; ++s) w[it][s] = ldw(p + s * 256);
+    }
+    const float sa = EPI != IE_EPI_I32 ? sA[m_c] : 0.0f;
+    EpiIn e[IPW];
+#pragma unroll
+    for (int it = 0; it < IPW; ++it) e[it] = epi_load<EPI>(m_c, min(4 * (i0 + it) + f, N - 1), N, sB, bias, residual);
+#pragma unroll
+    for (int c = 0; c < SPT; ++c) {
+        const int ch = threadIdx.x + 256 * c;
+        if (CH % 256 == 0 || ch < CH) {
+            const int r = ch / (K / 16);
+            reinterpret_cast<i32x4*>(a_lds + r * LDA)[ch - r * (K / 16)] = stage[c];
+        }
+    }
+    __syncthreads();
+
+    const int8_t* arow[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) arow[j] = a_lds + min(4 * j + f, M - 1) * LDA + kofs;
+#pragma unroll
+    for (int it = 0; it < IPW; ++it) {
+        if (i0 + it >= nitems_all) continue;  // uniform: past the last item
+        i32x4 acc[MB][2];
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[j][0] = acc[j][1] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int j = 0; j < MB; ++j)
+                acc[j][s & 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    *reinterpret_cast<const i32x4*>(arow[j] + s * 256), w[it][s], acc[j][s & 1], 0, 0, 0);
+        // diagonal entries (row part == column part), summed over the quad
+        int32_t mine = 0;
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            const i32x4 x4 = acc[j][0] + acc[j][1];
+            int32_t x = part == 0 ? x4[0] : part == 1 ? x4[1] : part == 2 ? x4[2] : x4[3];
+            x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xf, 0xf, false);  // quad_perm [1, 0, 3, 2]
+            x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xf, 0xf, false);  // quad_perm [2, 3, 0, 1]
+            mine = part == j ? x : mine;
+        }
+        const int n = 4 * (i0 + it) + f;
+        if (out_ok && n < N) gemv_store<EPI>(C, out_m, n, N, mine, sa, e[it], 0, GemvFusion{});
+    }
+}
+
 // Any K % 4 == 0 and any alignment: one thread per output element.
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
@@ -841,6 +938,23 @@ void launch_parted(const GemmArgs& a, hipStream_t s) {
     else go(std::integral_constant<int, 4>{});
 }
 
+template <int EPI, int S>
+void launch_burst(const GemmArgs& a, hipStream_t s) {
+    constexpr int IPW = S <= 3 ? 8 : 2;  // 24 loads of weights per lane in flight
+    const int items = (a.N + 3) / 4;
+    const unsigned blocks = (unsigned)((items + 4 * IPW - 1) / (4 * IPW));
+    const bool nt = (size_t)a.N * (256 * S) >= kStreamWeightBytes;
+    auto go = [&](auto mb) {
+        constexpr int MB = decltype(mb)::value;
+        auto* k = nt ? gemv_i8_burst_kernel<EPI, true, MB, S, IPW> : gemv_i8_burst_kernel<EPI, false, MB, S, IPW>;
+        k<<<blocks, 256, 0, s>>>(a.M, a.N, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
+                                 a.sA, a.sB, a.bias, a.residual, a.C);
+    };
+    if (a.M <= 4) go(std::integral_constant<int, 1>{});
+    else if (a.M <= 8) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 4>{});
+}
+
 template <int EPI, int K, int SRC>
 void launch_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s) {
     if (a.M <= 1) launch_fixed<1, EPI, K / 16, SRC>(a, s, f);
@@ -851,6 +965,14 @@ void launch_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s) {
 
 template <int MT, int EPI>
 void launch_mt(const GemmArgs& a, hipStream_t s) {
+    // Wide GPT-2-width GEMVs (the 768 x 50257 LM head): all of a wave's
+    // loads at once (M = 1 / 4 / 8: 0.49 / 0.44 / 0.39 -> 0.52 / 0.51 / 0.49
+    // of HBM peak per graph-replayed launch; level at M = 16, and slower on
+    // the narrow shapes, whose time is launch latency).
+    if (a.N >= 16384 && a.M <= 8) {
+        if (a.K == 768) return launch_burst<EPI, 3>(a, s);
+        if (a.K == 3072) return launch_burst<EPI, 12>(a, s);
+    }
     if constexpr (MT > 4) {
         if (a.K == 768) return launch_mfma16<EPI, 12>(a, s);
         if (a.K == 3072) return launch_mfma16<EPI, 48>(a, s);
