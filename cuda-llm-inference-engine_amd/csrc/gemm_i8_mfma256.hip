@@ -207,6 +207,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     // store loop, each would wait for all earlier stores (vmcnt counts stores,
     // and C may alias them).  Two waves per SIMD leave no room for all 64 row
     // scales beside the accumulators, so they are gathered one block at a time.
+    // C goes out as non-temporal stores (2316 against 2187 TOP/s at 8192^3
+    // with the stores cached in L2).
     const int h = lane >> 5;
     const int rbase = m0 + wm * 128 + 4 * h;
     const int cbase = n0 + wn * 32 * NJ + (lane & 31);
