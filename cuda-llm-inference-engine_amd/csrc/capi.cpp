@@ -76,7 +76,7 @@ int ie_init(void) {
     if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return ie::fail(IE_ERR_UNSUPPORTED, "ie_init: device %d is %s, the library is built for gfx950",
                         dev, p.gcnArchName);
-    return IE_OK;
+    return ie::compat_sampler_init();
 }
 
 int ie_quantize_fp32_to_int8(int rows, int cols, const float* input, int32_t* output_packed,
@@ -325,6 +325,15 @@ int ie_topk(int rows, const float* logits, int n, int k, float* out_vals, int* o
     if (!logits || !out_vals || !out_idx) return ie::fail(IE_ERR_INVALID, "topk: null pointer");
     ie::launch_topk(rows, logits, n, k, out_vals, out_idx, (hipStream_t)stream);
     return ie::check_launch("topk");
+}
+
+int ie_check_token_ids(int n, const int* ids, int vocab_size) {
+    if (n < 0 || vocab_size <= 0) return ie::fail(IE_ERR_INVALID, "token ids: n=%d vocab_size=%d", n, vocab_size);
+    if (n > 0 && !ids) return ie::fail(IE_ERR_INVALID, "token ids: null pointer");
+    for (int i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= vocab_size)
+            return ie::fail(IE_ERR_INVALID, "token id %d at index %d is outside [0, %d)", ids[i], i, vocab_size);
+    return IE_OK;
 }
 
 }  // extern "C"

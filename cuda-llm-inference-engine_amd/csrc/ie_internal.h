@@ -160,6 +160,9 @@ void launch_argmax(int rows, const float* logits, int n, int* out,
 
 // ---- top-k sampler (sampler.hip, host/sampler.cpp) ----
 constexpr int kTopkMax = 1024;  // largest k selected on the device
+// Makes the device and pinned buffers of sample_argmax / sample_top_k
+// (called by ie_init, so the compat samplers allocate nothing afterwards).
+int compat_sampler_init();
 void launch_topk(int rows, const float* logits, int n, int k, float* out_vals,
                  int* out_idx, hipStream_t s);
 

@@ -563,8 +563,15 @@ struct GPT2Engine::Impl {
         ++pos;
     }
 
+    // Host token ids index wte rows on the device without a bound: reject
+    // any outside [0, vocab_size) before they are uploaded.
+    void check_ids(const int* t, size_t n) const {
+        if (ie_check_token_ids((int)n, t, cfg.vocab_size) != IE_OK) throw std::runtime_error(ie_last_error());
+    }
+
     // Upload one token per sequence, run a step, fetch the argmax ids.
     void step_tokens(const int* toks, int B, bool fetch) {
+        check_ids(toks, B);
         std::memcpy(host_tokens, toks, sizeof(int) * B);
         HIPC(hipMemcpyAsync(tokens, host_tokens, sizeof(int) * B, hipMemcpyHostToDevice, stream));
         run_step(B);
@@ -623,6 +630,7 @@ struct GPT2Engine::Impl {
         if (P < 1) throw std::runtime_error("empty prompt");
         if (!prefill_applies()) throw std::runtime_error("prefill needs d_head 64 or 128");
         if (pos + P > cfg.max_seq_len) throw std::runtime_error("prompt does not fit the context");
+        check_ids(toks, (size_t)B * P);
         const int d = cfg.d_model, ff = cfg.d_ff, H = cfg.n_heads, dh = cfg.d_head;
         const int chunk = std::min(P, prefill_chunk(B));
         ensure_prefill(B * chunk);
@@ -695,11 +703,15 @@ struct GPT2Engine::Impl {
         return w + kv;
     }
 
-    void fill_tail_metrics(InferenceMetrics& m, const std::vector<float>& itl, float decode_ms, int B) {
+    // tps counts the tokens the decode steps produced for sequences still
+    // running (a sequence past its EOS is carried by the batch step but emits
+    // nothing); mbu counts the bytes every step streams.
+    void fill_tail_metrics(InferenceMetrics& m, const std::vector<float>& itl, float decode_ms, int B,
+                           long decode_tokens) {
         const int n = (int)itl.size();
         if (n > 0) {
             m.tpot_ms = decode_ms / n;
-            m.tps = 1000.0f * n * B / decode_ms;
+            m.tps = 1000.0f * decode_tokens / decode_ms;
             m.itl_min_ms = *std::min_element(itl.begin(), itl.end());
             m.itl_max_ms = *std::max_element(itl.begin(), itl.end());
             auto sorted = itl;
@@ -788,6 +800,7 @@ void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tok
     metrics.max_tokens = max_new_tokens;
     metrics.generating = true;
     if (prompt_tokens.empty()) throw std::runtime_error("empty prompt");
+    I.check_ids(prompt_tokens.data(), prompt_tokens.size());
     if (reset_kv) I.reset();
     // Seeds as the reference's loop passes them: 42 for the token after the
     // prompt, then 43, 44, ... (src/gpt2_engine.cu:707, 713, 747).
@@ -822,7 +835,7 @@ void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tok
         itl.push_back(dt);
         decode_ms += dt;
     }
-    I.fill_tail_metrics(metrics, itl, decode_ms, 1);
+    I.fill_tail_metrics(metrics, itl, decode_ms, 1, (long)itl.size());
     metrics.end_to_end_ms = ms_since(t_total);
     metrics.generating = false;
 }
@@ -834,8 +847,10 @@ void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, in
     const int B = (int)prompts.size();
     if (B < 1 || B > I.opt.max_batch) throw std::runtime_error("batch out of range");
     const size_t P = prompts[0].size();
-    for (const auto& p : prompts)
+    for (const auto& p : prompts) {
         if (p.size() != P || P == 0) throw std::runtime_error("prompts must share one non-zero length");
+        I.check_ids(p.data(), P);
+    }
     metrics = InferenceMetrics{};
     metrics.max_tokens = max_new_tokens;
     metrics.generating = true;
@@ -849,6 +864,7 @@ void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, in
     std::vector<float> itl;
     float decode_ms = 0.0f;
     std::vector<char> done(B, 0);
+    long decode_tokens = 0;
     for (int stepi = 0; stepi < max_new_tokens; ++stepi) {
         bool all_done = true;
         for (int b = 0; b < B; ++b) {
@@ -861,6 +877,7 @@ void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, in
         if (all_done || stepi + 1 == max_new_tokens || I.pos >= I.cfg.max_seq_len) break;
         // The argmax of the previous step is already in the device token
         // buffer: the step reads it directly, only the ids come back.
+        for (int b = 0; b < B; ++b) decode_tokens += done[b] ? 0 : 1;
         const auto t = Clock::now();
         I.run_step(B);
         HIPC(hipMemcpyAsync(I.host_tokens, I.tokens, sizeof(int) * B, hipMemcpyDeviceToHost, I.stream));
@@ -869,7 +886,7 @@ void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, in
         itl.push_back(dt);
         decode_ms += dt;
     }
-    I.fill_tail_metrics(metrics, itl, decode_ms, B);
+    I.fill_tail_metrics(metrics, itl, decode_ms, B, decode_tokens);
     metrics.end_to_end_ms = ms_since(t_total);
     metrics.generating = false;
 }

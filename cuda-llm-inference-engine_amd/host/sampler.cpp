@@ -61,8 +61,9 @@ int draw(const float* vals, const int* idx, int k, float temperature, float r) {
     return idx[k - 1];
 }
 
-// Device and pinned host buffers of the compat samplers, made on first use
-// and kept for the process (the reference allocates a host vector per call).
+// Device and pinned host buffers of the compat samplers, made by ie_init()
+// (or by a sampler's first call when ie_init was not called) and kept for the
+// process (the reference allocates a host vector per call).
 // k values then k indices in one buffer, so one transfer brings both back.
 struct CompatBufs {
     std::mutex mu;
@@ -83,6 +84,14 @@ CompatBufs& compat_bufs() {
 }
 
 }  // namespace
+
+namespace ie {
+int compat_sampler_init() {
+    CompatBufs& b = compat_bufs();
+    std::lock_guard<std::mutex> lock(b.mu);
+    return b.ready() ? IE_OK : fail(IE_ERR_HIP, "ie_init: sampler buffer allocation failed");
+}
+}  // namespace ie
 
 extern "C" int ie_top_k_draw(const float* vals, const int* idx, int k, float temperature, unsigned int seed,
                              int* token) {

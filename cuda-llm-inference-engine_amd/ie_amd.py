@@ -46,6 +46,7 @@ SIGNATURES = {
     "ie_argmax": (_I, [_I, _P, _I, _P, _P]),
     "ie_topk": (_I, [_I, _P, _I, _I, _P, _P, _P]),
     "ie_top_k_draw": (_I, [_P, _P, _I, _F, ctypes.c_uint, _P]),
+    "ie_check_token_ids": (_I, [_I, _P, _I]),
 }
 
 # include/ie_engine.h

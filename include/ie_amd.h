@@ -76,8 +76,10 @@ typedef enum { IE_KV_F32 = 0, IE_KV_BF16 = 1 } ie_kv_dtype;
 
 const char* ie_last_error(void);
 int ie_version(void);
-/* Optional: binds the current device, checks it is gfx950.  Entry points call
- * it lazily; calling it first keeps all one-time work out of timed regions. */
+/* Optional: checks that the current device is gfx950 and makes the two small
+ * buffers of the compat samplers (sample_argmax / sample_top_k in
+ * ie_compat.h), so nothing allocates afterwards; calling it first also keeps
+ * the HIP runtime's one-time start-up out of timed regions. */
 int ie_init(void);
 
 /* Per-row symmetric quantizer: scales[r] = max|x_r|/127 (1 for a zero row),
@@ -192,6 +194,13 @@ int ie_topk(int rows, const float* logits, int n, int k, float* out_vals,
  * untouched.  *token = the chosen index. */
 int ie_top_k_draw(const float* vals, const int* idx, int k, float temperature,
                   unsigned int seed, int* token);
+
+/* Host-side check of token ids before they reach a device embedding
+ * (ie_embedding* index wte rows without a bound, as run_embedding does,
+ * kernels/layernorm/15_embed.cu:4-21): IE_OK when every ids[i], i < n, lies
+ * in [0, vocab_size); otherwise IE_ERR_INVALID naming the first offender.
+ * No HIP call.  The engine runs it on every host token it is given. */
+int ie_check_token_ids(int n, const int* ids, int vocab_size);
 
 #ifdef __cplusplus
 }

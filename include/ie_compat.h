@@ -72,8 +72,9 @@ void run_embedding(const int* token_ids, int seq_len, int start_pos,
  * pairs (top-k) come back instead of the whole row; k is clamped to
  * vocab_size as in the reference and must then be <= IE_TOPK_MAX.  The draw
  * follows the reference's float arithmetic and its srand(seed) / rand() rule
- * with a generator private to the library (see ie_top_k_draw).  Two small
- * device buffers are allocated on the first call and kept.  -1 on error. */
+ * with a generator private to the library (see ie_top_k_draw).  Their two
+ * small buffers (device and pinned host) are made by ie_init(), or by the
+ * first call when ie_init() was not called, and kept.  -1 on error. */
 int sample_argmax(const float* d_logits, int vocab_size);
 int sample_top_k(const float* d_logits, int vocab_size, int k,
                  float temperature, unsigned int seed);

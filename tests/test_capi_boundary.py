@@ -16,7 +16,7 @@ COMPAT = os.path.join(ROOT, "include", "ie_compat.h")
 LIB = os.path.join(PKG, "libie_amd.so")
 
 
-SIGS_EXPECTED = 20  # entry points declared in include/ie_amd.h
+SIGS_EXPECTED = 21  # entry points declared in include/ie_amd.h
 
 
 def declared_c_functions(path=HDR):

@@ -61,3 +61,21 @@ def test_engine_c_api_rejects_bad_arguments_without_a_gpu(ie):
     st = lib.ie_engine_create(ctypes.byref(h), None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, -5)
     assert st == ie.IE_ERR_INVALID and "prefill_chunk" in ie.last_error()
     assert lib.ie_engine_create(None, None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, 0) == ie.IE_ERR_INVALID
+
+
+def test_token_id_check_rejects_out_of_range(ie):
+    """ie_check_token_ids, which the engine runs on every host token before it
+    is uploaded (the embedding kernels index wte rows without a bound)."""
+    import ctypes
+
+    V = 1000
+    for bad, where in (([5, -1, 7], 1), ([V, 0], 0), ([0, 1, 2, V + 3], 3)):
+        arr = (ctypes.c_int * len(bad))(*bad)
+        st = ie.call("ie_check_token_ids", len(bad), ctypes.cast(arr, ctypes.c_void_p), V)
+        assert st == ie.IE_ERR_INVALID
+        assert f"index {where}" in ie.last_error() and str(bad[where]) in ie.last_error()
+    ok = (ctypes.c_int * 3)(0, V - 1, 17)
+    assert ie.call("ie_check_token_ids", 3, ctypes.cast(ok, ctypes.c_void_p), V) == ie.IE_OK
+    assert ie.call("ie_check_token_ids", 0, None, V) == ie.IE_OK
+    assert ie.call("ie_check_token_ids", 2, None, V) == ie.IE_ERR_INVALID
+    assert ie.call("ie_check_token_ids", 1, ctypes.cast(ok, ctypes.c_void_p), 0) == ie.IE_ERR_INVALID
