@@ -802,7 +802,7 @@ constexpr long long kWaveSplitUnits = 1024;
 // Batches up to this size use the balanced partition for one-wave splits
 // (every workgroup scans the context lengths twice).
 constexpr int kBalancedMaxB = 4096;
-// At most this many (b, kv head, split) units count as few.
+// At most this many (kv head, split) units per sequence count as few.
 constexpr long long kFewUnits = 64;
 
 // Workgroups of `threads` threads of kernel f resident per CU (at least 1),
@@ -862,13 +862,15 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
                                            a.num_blocks_per_seq, a.num_splits, nbmax, qscale, a.workspace);
         return;
     }
-    // Few units (GPT-2 at batch 1: 12 heads, one split): 8 waves share each
-    // split, so a wave walks half as many chunks one after another; measured
-    // +2.4% decode tok/s at batch 1 (16 waves: +1%), where it fits without
-    // spilling (G <= 4).
+    // Few units per sequence (GPT-2: 12 heads, one to three splits): 8 waves
+    // share each split, so a wave walks half as many chunks one after
+    // another; measured +2.4% decode tok/s at batch 1 (16 waves: +1%) and
+    // +1.1% at batch 16, where it fits without spilling (G <= 4).  The count
+    // is decided per sequence, not per batch, so a sequence's output has the
+    // same bits at every batch size (the engine's batch invariance).
     constexpr int WF = 8;
     constexpr bool WF_FITS = G <= 4;
-    const bool few = WF_FITS && !wave && (long long)a.num_splits * a.H_kv * a.B <= kFewUnits;
+    const bool few = WF_FITS && !wave && (long long)a.num_splits * a.H_kv <= kFewUnits;
     using KernelT = decltype(&decode_attn_split_kernel<D, G, KV, 4, true, 2, 256>);
     KernelT k = wave ? (bs16 ? decode_attn_split_kernel<D, G, KV, 1, true, RW, NTW>
                              : decode_attn_split_kernel<D, G, KV, 1, false, RW, NTW>)

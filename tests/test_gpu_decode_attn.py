@@ -93,6 +93,44 @@ def test_ctx32768_subset(ie, orc):
         assert rel_err(got64, want) < REL
 
 
+@pytest.mark.parametrize("kvdt", [0, 1])
+def test_cfg4_ctx32768_full_batch(ie, orc, kvdt):
+    """BASELINE configs[3] at ctx 32768 and its full batch: B = 32, Hq 32 /
+    Hkv 8, d 128, lengths U[16384, 32768], shuffled block table, fp32 and
+    bf16 KV (~6.4 GB of fp32 K+V).  The cache is drawn on the device and
+    copied to the host for the full oracle; the reference split rule (16
+    splits) and a 64-split plan."""
+    import torch
+
+    r = rng(32768 + 10 * kvdt)
+    B, H_q, H_kv, d, ctx, bs = 32, 32, 8, 128, 32768, 16
+    lens = r.integers(ctx // 2, ctx + 1, B)
+    lens[3] = ctx
+    nbs = (lens + bs - 1) // bs
+    P, nbps = int(nbs.sum()), int(nbs.max())
+    perm = r.permutation(P).astype(np.int32)
+    table = np.zeros((B, nbps), np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :nbs[b]] = perm[off:off + nbs[b]]
+        off += int(nbs[b])
+    g = torch.Generator(device="cuda").manual_seed(int(r.integers(1 << 30)))
+    kc = torch.randn((P, bs, H_kv, d), device="cuda", generator=g)
+    vc = torch.randn((P, bs, H_kv, d), device="cuda", generator=g)
+    if kvdt:
+        kc = kc.to(torch.bfloat16).view(torch.int16)
+        vc = vc.to(torch.bfloat16).view(torch.int16)
+    Q = r.standard_normal((B, H_q, d)).astype(np.float32)
+    kh = kc.cpu().numpy().view(np.uint16) if kvdt else kc.cpu().numpy()
+    vh = vc.cpu().numpy().view(np.uint16) if kvdt else vc.cpu().numpy()
+    want = orc.decode_attn(Q, kh, vh, table, lens, ctx, bs, H_kv, kv_dtype=kvdt)
+    del kh, vh
+    for splits in (0, 64):
+        got = host(ie.decode_attn(dev(Q), kc, vc, dev(table), dev(lens.astype(np.int32)), ctx, bs, H_kv,
+                                  kv_dtype=kvdt, splits=splits))
+        assert rel_err(got, want) < REL, splits
+
+
 def test_bf16_vs_fp32_inputs_stated_bound(ie, orc):
     r = rng(77)
     B, H_q, H_kv, d, ctx = 4, 32, 8, 128, 2048
@@ -171,10 +209,12 @@ def test_one_wave_and_four_wave_splits(ie, orc, G, d, kvdt):
 @pytest.mark.parametrize("kvdt", [0, 1])
 @pytest.mark.parametrize("G", [1, 4])
 def test_four_wave_splits_with_many_units(ie, orc, G, kvdt):
-    """More than 64 (b, head, split) units of short splits (under 256 tokens
-    each): four waves per split (B 8 x 4 KV heads x 3 splits = 96 units)."""
+    """More than 64 (kv head, split) units per sequence of short splits
+    (under 256 tokens each): four waves per split (8 KV heads x 11 splits =
+    88 units); with 3 splits (24 units) eight waves.  The wave count depends
+    on the sequence's units only, so the batch does not change it."""
     r = rng(1100 + G + kvdt)
-    B, H_kv, d = 8, 4, 64
+    B, H_kv, d = 8, 8, 64
     lens = r.integers(100, 701, B)
     kc, vc, table, _, _ = make_paged_cache(r, B, H_kv, d, lens, 16)
     Q = r.standard_normal((B, H_kv * G, d)).astype(np.float32)
@@ -182,8 +222,14 @@ def test_four_wave_splits_with_many_units(ie, orc, G, kvdt):
         kc, vc = bf16_bits(kc), bf16_bits(vc)
     mx = int(lens.max())
     want = orc.decode_attn(Q, kc, vc, table, lens, mx, 16, H_kv, kv_dtype=kvdt)
-    got = run_gpu(ie, Q, kc, vc, table, lens, mx, 16, H_kv, kv_dtype=kvdt, splits=3)
-    assert rel_err(got, want) < REL
+    for splits in (11, 3):
+        got = run_gpu(ie, Q, kc, vc, table, lens, mx, 16, H_kv, kv_dtype=kvdt, splits=splits)
+        assert rel_err(got, want) < REL, splits
+        # each sequence alone gives the same bits as inside the batch
+        for b in (0, 5):
+            one = run_gpu(ie, Q[b:b + 1], kc, vc, table[b:b + 1], lens[b:b + 1], mx, 16, H_kv, kv_dtype=kvdt,
+                          splits=splits)
+            assert np.array_equal(one[0], got[b]), (splits, b)
 
 
 def test_edges(ie, orc):

@@ -138,18 +138,19 @@ def test_gpt2_small_random_generates(ie):
 
 
 def check_steps(errs):
-    """Per-step max |diff| / max |logits| for the 768-wide model.  At this
-    width an activation now and then lies within fp32-vs-fp64 noise of an int8
-    rounding boundary and is quantized one step apart; the step's K/V then stay
-    in the cache, so the sequence's later logits move too.  Running the oracle
-    itself with 1e-7 relative noise on its LayerNorm outputs (3 sequences x 60
-    steps, this model) moves logits by up to 2.1e-2 of their scale, and the
-    device shows the same events.  Bar: every step within 3e-2, and steps
-    before the first such event within fp32 rounding (1e-5)."""
+    """Per-step max |diff| / max |logits| of a free-running engine against the
+    free-running oracle, 768-wide model.  At this width an activation now and
+    then lies within fp32-vs-fp64 noise of an int8 rounding boundary and is
+    quantized one step apart; the step's K/V then stay in the cache, so the
+    sequence's later logits move too.  Running the oracle itself with 1e-7
+    relative noise on its LayerNorm outputs (3 sequences x 60 steps, this
+    model) moves logits by up to 2.1e-2 of their scale, and the device shows
+    the same events.  Bar: every step within 3e-2.  This is a drift bound for
+    long free runs; the op-by-op parity bar (every op on the device's own
+    inputs, bit-exact or within 1e-5) is test_gpu_engine_parity.py's
+    teacher-forced test."""
     errs = np.asarray(errs)
     assert errs.max() <= 3e-2, errs
-    first = int(np.argmax(errs > 1e-5)) if (errs > 1e-5).any() else len(errs)
-    assert (errs[:first] <= 1e-5).all()
 
 
 def check_vs_oracle(ie, model_dir, B, steps, seed, eng_kw, orc_kw):
@@ -344,3 +345,114 @@ def test_generate_uses_prefill_and_matches_stepwise_prompt(ie, mid_dir):
     tb, mb = b.generate(prompt, 4, ignore_eos=True)
     assert a.session_tokens() == b.session_tokens() == 64 + 3
     assert ma["ttft_ms"] < mb["ttft_ms"]
+
+
+# ---------------------------------------------------------------- EOS, sessions
+EOS = 50256
+
+
+def echo_model(path, eos_from):
+    """Zero-weight model over the GPT-2 vocabulary (one layer, d 64): the
+    final hidden row at position p is wte[t] + wpe[p].  wte rows are N(0, 1),
+    so LN(wte[t]) . wte[t] ~ 64 beats every other row (~8 per unit of
+    Gaussian tail, under 40 over 50k rows) and greedy decoding repeats its
+    input; from position eos_from on, wpe adds 20 wte[EOS] and <|endoftext|>
+    wins.  Returns the tensors."""
+    from gpt2_model import random_tensors, write_model
+
+    cfg = dict(n_layers=1, n_heads=1, d_model=64, d_ff=64, vocab_size=EOS + 1, max_seq_len=128)
+    t = random_tensors(cfg, 77, zero_weights=True, zero_biases=True, ln_jitter=0)
+    t["wte"] = np.random.default_rng(78).standard_normal((EOS + 1, 64)).astype(np.float32)
+    t["wpe"] = np.zeros((128, 64), np.float32)
+    t["wpe"][eos_from:] = 20 * t["wte"][EOS]
+    write_model(str(path), cfg, t, fp32_weights=False)
+    return t
+
+
+def echo_expected(t, last_token, last_pos, max_new):
+    """Greedy continuation from the token at last_pos, in float64 (the closed
+    form of the zero-weight model); every pick's top-2 gap must be wide."""
+    out, tok, p = [], last_token, last_pos
+    while len(out) < max_new:
+        x = (t["wte"][tok] + t["wpe"][p]).astype(np.float64)
+        xf = (x - x.mean()) / np.sqrt(x.var() + 1e-5)
+        logits = t["wte"].astype(np.float64) @ xf
+        top = np.sort(logits)[-2:]
+        assert top[1] - top[0] > 5.0
+        nxt = int(np.argmax(logits))
+        if nxt == EOS:
+            break
+        out.append(nxt)
+        tok, p = nxt, p + 1
+    return out
+
+
+def test_eos_stops_generation(ie, tmp_path):
+    """tests/test_engine.cu:65-74 (EosStopsGeneration): generation ends at
+    <|endoftext|> (src/gpt2_engine.cu:717) after at least one token and within
+    max_new; greedy, sampled and batched."""
+    P, eos_from = 12, 20
+    t = echo_model(tmp_path / "echo", eos_from)
+    prompt = np.random.default_rng(5).integers(0, EOS, P).astype(np.int32)
+    want = echo_expected(t, int(prompt[-1]), P - 1, 64)
+    assert 0 < len(want) < 64 and len(want) == eos_from - P + 1
+    eng = ie.Engine(tmp_path / "echo", max_batch=2)
+    got, m = eng.generate_one(prompt, 64, greedy=True)
+    assert got == want and m["tokens_generated"] == len(want)
+    got_s, _ = eng.generate_one(prompt, 64, temperature=0.8, top_k=40, greedy=False)
+    assert got_s == want
+    prompts = np.stack([prompt, np.roll(prompt, 1)])
+    out, m = eng.generate(prompts, 64)
+    for b in range(2):
+        w = echo_expected(t, int(prompts[b, -1]), P - 1, 64)
+        assert out[b, :len(w)].tolist() == w and (out[b, len(w):] == -1).all()
+    eng.close()
+
+
+def test_session_continuation_positions(ie, tmp_path):
+    """generate(..., reset_kv=false) continues the session
+    (src/gpt2_engine.cu:680-698): the new prompt's positions follow the cached
+    ones, so <|endoftext|> arrives where the position law puts it."""
+    t = echo_model(tmp_path / "echo", 40)
+    r = np.random.default_rng(6)
+    p1, p2 = r.integers(0, EOS, 10).astype(np.int32), r.integers(0, EOS, 20).astype(np.int32)
+    eng = ie.Engine(tmp_path / "echo", max_batch=1)
+    t1, _ = eng.generate_one(p1, 3, greedy=True, reset=True)
+    assert t1 == echo_expected(t, int(p1[-1]), 9, 3) and eng.session_tokens() == 13
+    t2, _ = eng.generate_one(p2, 64, greedy=True, reset=False)
+    want = echo_expected(t, int(p2[-1]), 13 + 20 - 1, 64)
+    # picks from positions 32 .. 39 repeat the last prompt token; 40 gives EOS
+    assert t2 == want and len(want) == 40 - 32
+    assert eng.session_tokens() == 33 + len(want)  # every emitted token was fed
+    eng.close()
+
+
+@pytest.mark.parametrize("prefill", [True, False])
+def test_session_continuation_attends_to_the_cache(ie, mid_dir, prefill):
+    """A continuation prompt attends to the cached session: the engine's
+    greedy picks across two generate() calls (the second with reset=False,
+    through prefill or, as the reference does, through decode steps) equal the
+    oracle's argmax over the whole token history, fed one position at a time,
+    wherever the oracle's top-2 gap exceeds 6e-2 of the logit scale."""
+    from oracle.gpt2_step import OracleGPT2
+
+    r = np.random.default_rng(91)
+    p1, p2 = r.integers(0, 1000, 20).astype(np.int32), r.integers(0, 1000, 15).astype(np.int32)
+    eng = ie.Engine(mid_dir, max_batch=1, prefill=prefill)
+    t1, _ = eng.generate_one(p1, 6, greedy=True, reset=True)
+    t2, _ = eng.generate_one(p2, 6, greedy=True, reset=False)
+    assert len(t1) == len(t2) == 6 and eng.session_tokens() == 20 + 6 + 15 + 6
+    eng.close()
+    seq = list(p1) + t1 + list(p2) + t2
+    picks = {19 + j: t1[j] for j in range(6)}
+    picks.update({40 + j: t2[j] for j in range(6)})
+    om = OracleGPT2(str(mid_dir), batch=1)
+    checked = 0
+    for p, tok in enumerate(seq):
+        want = om.step(np.array([tok], np.int32))[0]
+        if p in picks:
+            top = np.sort(want)[-2:]
+            if top[1] - top[0] > 6e-2 * np.abs(want).max():
+                assert picks[p] == int(np.argmax(want)), p
+                checked += 1
+    assert checked >= 6

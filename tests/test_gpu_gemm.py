@@ -320,6 +320,31 @@ def test_8192_cube_sampled_rows_and_checksum(ie, orc):
     assert np.array_equal(C[torch.from_numpy(rows).cuda()].cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
+def test_cfg2_m512_lm_head_shape_full(ie, orc, epi):
+    """M = 512 activations x the 768 x 50257 LM-head
+    weights (the 256x256-tile kernel, N % 256 = 81), the whole output against
+    the oracle: int32 and Plain / Bias / Residual bit-exact, GELU 2e-6."""
+    M, K, N = 512, 768, 50257
+    A, W = problem(M, N, K, 512 + epi)
+    r = rng(55 + epi)
+    bias = (r.standard_normal(N) * 0.5).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    if epi == 4:
+        got = host(ie.int8_gemm(dev(Ap), dev(Wp), epilogue=ie.EPI_I32))
+        assert np.array_equal(got, orc.gemm_i32(Ap, Wp))
+        return
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi,
+                            dev(bias) if epi else None, dev(res) if epi == 3 else None))
+    want = orc.gemm(Ap, Wp, sA, sW, epi, bias if epi else None, res if epi == 3 else None)
+    if epi == 2:
+        assert np.allclose(got, want, rtol=2e-6, atol=1e-7), np.abs(got - want).max()
+    else:
+        assert np.array_equal(got, want), np.abs(got - want).max()
+
+
 # ------------------------------------------------------------------ 256x256 tiles
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (3000, 5000, 512), (2304, 8192, 768),
                                    (8192, 3000, 256)])
