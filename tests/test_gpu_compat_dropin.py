@@ -1,0 +1,137 @@
+"""The drop-in C++ entry points (include/ie_compat.h) called for results from
+a plain C++ program (tests/compat_dropin.cpp, built by the package Makefile)
+that links libie_amd.so the way a restated reference engine or test would:
+the reference's own signatures, the null stream, its [B, H_q, 16, d + 2]
+decode workspace, residual aliased to C, LayerNorm in place.
+
+It restates tests/test_int8_gemm.cu:15-94 (srand(42) inputs, quantize A and
+B^T, run_int8_gemm; the reference's bound max |INT8 - FP32| < 0.012 sqrt(K))
+and tests/test_decode_attention.cu:48-140 (srand(42) Q/K/V, identity-table
+paged cache, max |diff| < 1e-5), and calls run_int8_gemm_bias /
+_bias_gelu / _bias_residual, run_layernorm, run_embedding,
+run_flash_attn_v2, sample_argmax and sample_top_k.  Here each output is
+checked against the oracle on the program's own inputs: quantizer, int32-exact
+GEMMs and embedding bit-exact, GELU 2e-6, attention 1e-5 absolute (the
+reference's bar), LayerNorm 1e-5 of scale, sampled ids equal.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import PKG
+
+pytestmark = pytest.mark.gpu
+
+EXE = os.path.join(PKG, "_build", "compat_dropin")
+
+
+@pytest.fixture(scope="module")
+def run_dir(tmp_path_factory):
+    if not os.path.exists(EXE):
+        pytest.fail(f"{EXE} is missing: run __graft_entry__.build()")
+    d = tmp_path_factory.mktemp("dropin")
+    r = subprocess.run([EXE, str(d)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+    assert "rejected" not in r.stderr, r.stderr
+    cases = [ln.split() for ln in open(d / "manifest.txt")]
+    return d, cases
+
+
+def load(d, case, name, dt, shape=None):
+    a = np.fromfile(os.path.join(d, f"{case}_{name}.bin"), dtype=dt)
+    return a if shape is None else a.reshape(shape)
+
+
+def cases_of(run, kind):
+    return [c for c in run[1] if c[0] == kind]
+
+
+def test_int8_gemm_reference_cases(orc, run_dir):
+    d = run_dir[0]
+    cases = cases_of(run_dir, "gemm")
+    assert len(cases) == 5
+    for _, cs, M, N, K in cases:
+        M, N, K = int(M), int(N), int(K)
+        A = load(d, cs, "A", np.float32, (M, K))
+        B = load(d, cs, "B", np.float32, (K, N))
+        # the program drew A then B with srand(42) / rand(), as the reference test
+        g = orc.GlibcRand(42)
+        assert np.array_equal(A.ravel(), g.uniform(M * K)) and np.array_equal(B.ravel(), g.uniform(K * N))
+        bias = load(d, cs, "bias", np.float32)
+        res = load(d, cs, "res", np.float32, (M, N))
+        Ap, sA = orc.quantize(A)
+        Bp, sB = orc.quantize(np.ascontiguousarray(B.T))
+        assert np.array_equal(load(d, cs, "A_packed", np.int32, (M, K // 4)), Ap)
+        assert np.array_equal(load(d, cs, "scale_A", np.float32), sA)
+        assert np.array_equal(load(d, cs, "BT_packed", np.int32, (N, K // 4)), Bp)
+        assert np.array_equal(load(d, cs, "scale_B", np.float32), sB)
+        C = load(d, cs, "C_plain", np.float32, (M, N))
+        assert np.array_equal(C, orc.gemm(Ap, Bp, sA, sB, 0)), cs
+        # the reference test's own acceptance bound against the fp32 GEMM
+        ref = A.astype(np.float64) @ B.astype(np.float64)
+        assert np.abs(C - ref).max() < 0.012 * np.sqrt(K), cs
+        assert np.array_equal(load(d, cs, "C_bias", np.float32, (M, N)), orc.gemm(Ap, Bp, sA, sB, 1, bias))
+        gelu = load(d, cs, "C_gelu", np.float32, (M, N))
+        assert np.allclose(gelu, orc.gemm(Ap, Bp, sA, sB, 2, bias), rtol=2e-6, atol=1e-7), cs
+        assert np.array_equal(load(d, cs, "C_residual", np.float32, (M, N)),
+                              orc.gemm(Ap, Bp, sA, sB, 3, bias, res)), cs
+
+
+def test_decode_attn_reference_cases(orc, run_dir):
+    d = run_dir[0]
+    cases = cases_of(run_dir, "attn")
+    assert len(cases) == 6
+    for _, cs, B, H_q, H_kv, ctx, dh, bs in cases:
+        B, H_q, H_kv, ctx, dh, bs = map(int, (B, H_q, H_kv, ctx, dh, bs))
+        nbps = (ctx + bs - 1) // bs
+        Q = load(d, cs, "Q", np.float32, (B, H_q, dh))
+        kc = load(d, cs, "k_cache", np.float32, (B * nbps, bs, H_kv, dh))
+        vc = load(d, cs, "v_cache", np.float32, (B * nbps, bs, H_kv, dh))
+        table = load(d, cs, "table", np.int32, (B, nbps))
+        lens = load(d, cs, "lens", np.int32)
+        O = load(d, cs, "O", np.float32, (B, H_q, dh))
+        want = orc.decode_attn(Q, kc, vc, table, lens, ctx, bs, H_kv)
+        assert np.abs(O - want).max() < 1e-5, (cs, np.abs(O - want).max())
+
+
+def test_layernorm_in_place_and_embedding(orc, run_dir):
+    d = run_dir[0]
+    (_, cs, rows, cols), = cases_of(run_dir, "layernorm")
+    rows, cols = int(rows), int(cols)
+    x = load(d, cs, "x", np.float32, (rows, cols))
+    want = orc.layernorm(x, load(d, cs, "gamma", np.float32), load(d, cs, "beta", np.float32))
+    got = load(d, cs, "out", np.float32, (rows, cols))
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    (_, cs, V, S, dm, seq, start), = cases_of(run_dir, "embedding")
+    V, S, dm, seq, start = map(int, (V, S, dm, seq, start))
+    want = orc.embedding(load(d, cs, "ids", np.int32), start, load(d, cs, "wte", np.float32, (V, dm)),
+                         load(d, cs, "wpe", np.float32, (S, dm)))
+    assert np.array_equal(load(d, cs, "out", np.float32, (seq, dm)), want)
+
+
+def test_flash_attn_v2(run_dir):
+    d = run_dir[0]
+    (_, cs, B, H, N, dh), = cases_of(run_dir, "flash")
+    B, H, N, dh = map(int, (B, H, N, dh))
+    Q, K, V = (load(d, cs, n, np.float32, (B, H, N, dh)).astype(np.float64) for n in ("Q", "K", "V"))
+    s = Q @ np.swapaxes(K, 2, 3) / np.sqrt(dh)
+    for name, causal in (("fa_full", False), ("fa_causal", True)):
+        t = np.where(np.tril(np.ones((N, N), bool)), s, -np.inf) if causal else s
+        p = np.exp(t - t.max(axis=-1, keepdims=True))
+        want = (p / p.sum(axis=-1, keepdims=True)) @ V
+        got = load(d, name, "O", np.float32, (B, H, N, dh))
+        assert np.abs(got - want).max() < 1e-5, (name, np.abs(got - want).max())
+
+
+def test_samplers(orc, run_dir):
+    d = run_dir[0]
+    (_, cs, n), = cases_of(run_dir, "sampler")
+    logits = load(d, cs, "logits", np.float32)
+    picks = load(d, cs, "picks", np.int32)
+    assert picks[0] == orc.argmax(logits) == 31337
+    # seed 42 reseeds, the repeated 42 draws the next rand(), 43 reseeds
+    assert picks[1] == orc.sample_top_k(logits, 40, 0.8, 42, skip=0)
+    assert picks[2] == orc.sample_top_k(logits, 40, 0.8, 42, skip=1)
+    assert picks[3] == orc.sample_top_k(logits, 40, 0.8, 43, skip=0)
