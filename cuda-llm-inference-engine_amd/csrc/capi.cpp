@@ -58,6 +58,39 @@ int check_launch(const char* what) {
     return IE_OK;
 }
 
+int check_decode_attn(int B, int H_q, int H_kv, int d, const float* Q, const void* k_cache, const void* v_cache,
+                      int kv_dtype, const int* block_table, const int* context_lens, int max_context_len,
+                      int block_size, int num_blocks_per_seq, const float* O, int num_splits, size_t* need_bytes,
+                      int* splits) {
+    *need_bytes = 0;
+    *splits = 1;
+    if (B < 0 || H_q <= 0 || H_kv <= 0 || d <= 0)
+        return fail(IE_ERR_INVALID, "decode_attn: bad sizes B=%d H_q=%d H_kv=%d d=%d", B, H_q, H_kv, d);
+    if (H_q % H_kv) return fail(IE_ERR_INVALID, "decode_attn: H_q=%d not a multiple of H_kv=%d", H_q, H_kv);
+    const int G = H_q / H_kv;
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return fail(IE_ERR_UNSUPPORTED, "decode_attn: group size %d not in {1,2,4,8}", G);
+    if (d != 64 && d != 128) return fail(IE_ERR_UNSUPPORTED, "decode_attn: head dim %d not in {64,128}", d);
+    if (kv_dtype != IE_KV_F32 && kv_dtype != IE_KV_BF16)
+        return fail(IE_ERR_INVALID, "decode_attn: unknown kv dtype %d", kv_dtype);
+    if (block_size <= 0) return fail(IE_ERR_INVALID, "decode_attn: block_size=%d", block_size);
+    if (max_context_len < 0) return fail(IE_ERR_INVALID, "decode_attn: max_context_len=%d", max_context_len);
+    const long long nb_max = ((long long)max_context_len + block_size - 1) / block_size;
+    if (num_blocks_per_seq < nb_max)
+        return fail(IE_ERR_INVALID, "decode_attn: num_blocks_per_seq=%d < ceil(max_context_len/block_size)=%lld",
+                    num_blocks_per_seq, nb_max);
+    if (B == 0) return IE_OK;
+    if (!Q || !O || !block_table || !context_lens || (nb_max > 0 && (!k_cache || !v_cache)))
+        return fail(IE_ERR_INVALID, "decode_attn: null pointer");
+    if (!aligned(Q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(O, 4))
+        return fail(IE_ERR_INVALID, "decode_attn: Q and the caches must be 16-byte aligned");
+    if ((long long)B * H_kv > 65535LL * 65535LL || B > 65535 || H_kv > 65535)
+        return fail(IE_ERR_UNSUPPORTED, "decode_attn: grid too large");
+    *splits = ie_decode_num_splits(max_context_len, block_size, num_splits);
+    *need_bytes = ie_decode_attn_workspace_bytes(B, H_q, d, *splits);
+    return IE_OK;
+}
+
 }  // namespace ie
 
 extern "C" {
@@ -76,7 +109,8 @@ int ie_init(void) {
     if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return ie::fail(IE_ERR_UNSUPPORTED, "ie_init: device %d is %s, the library is built for gfx950",
                         dev, p.gcnArchName);
-    return ie::compat_sampler_init();
+    const int st = ie::compat_sampler_init();
+    return st != IE_OK ? st : ie::decode_scratch_init();
 }
 
 int ie_quantize_fp32_to_int8(int rows, int cols, const float* input, int32_t* output_packed,
@@ -143,33 +177,17 @@ int ie_decode_attn(int B, int H_q, int H_kv, int d, const float* Q, const void* 
                    int num_blocks_per_seq, float* O, float* workspace, size_t workspace_bytes,
                    int num_splits, ie_stream_t stream) {
     using ie::fail;
-    if (B < 0 || H_q <= 0 || H_kv <= 0 || d <= 0)
-        return fail(IE_ERR_INVALID, "decode_attn: bad sizes B=%d H_q=%d H_kv=%d d=%d", B, H_q, H_kv, d);
-    if (H_q % H_kv) return fail(IE_ERR_INVALID, "decode_attn: H_q=%d not a multiple of H_kv=%d", H_q, H_kv);
-    const int G = H_q / H_kv;
-    if (G != 1 && G != 2 && G != 4 && G != 8)
-        return fail(IE_ERR_UNSUPPORTED, "decode_attn: group size %d not in {1,2,4,8}", G);
-    if (d != 64 && d != 128) return fail(IE_ERR_UNSUPPORTED, "decode_attn: head dim %d not in {64,128}", d);
-    if (kv_dtype != IE_KV_F32 && kv_dtype != IE_KV_BF16)
-        return fail(IE_ERR_INVALID, "decode_attn: unknown kv dtype %d", kv_dtype);
-    if (block_size <= 0) return fail(IE_ERR_INVALID, "decode_attn: block_size=%d", block_size);
-    if (max_context_len < 0) return fail(IE_ERR_INVALID, "decode_attn: max_context_len=%d", max_context_len);
-    const long long nb_max = ((long long)max_context_len + block_size - 1) / block_size;
-    if (num_blocks_per_seq < nb_max)
-        return fail(IE_ERR_INVALID, "decode_attn: num_blocks_per_seq=%d < ceil(max_context_len/block_size)=%lld",
-                    num_blocks_per_seq, nb_max);
-    if (B == 0) return IE_OK;
-    if (!Q || !O || !block_table || !context_lens || !workspace || (nb_max > 0 && (!k_cache || !v_cache)))
-        return fail(IE_ERR_INVALID, "decode_attn: null pointer");
-    if (!aligned(Q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(O, 4) ||
-        !aligned(workspace, 4))
-        return fail(IE_ERR_INVALID, "decode_attn: Q and the caches must be 16-byte aligned");
-    const int S = ie_decode_num_splits(max_context_len, block_size, num_splits);
-    const size_t need = ie_decode_attn_workspace_bytes(B, H_q, d, S);
+    size_t need = 0;
+    int S = 1;
+    const int st = ie::check_decode_attn(B, H_q, H_kv, d, Q, k_cache, v_cache, kv_dtype, block_table,
+                                         context_lens, max_context_len, block_size, num_blocks_per_seq, O,
+                                         num_splits, &need, &S);
+    if (st != IE_OK || B == 0) return st;
+    if (!workspace) return fail(IE_ERR_INVALID, "decode_attn: null pointer");
+    if (!aligned(workspace, 4)) return fail(IE_ERR_INVALID, "decode_attn: workspace must be 4-byte aligned");
     if (workspace_bytes < need)
         return fail(IE_ERR_WORKSPACE, "decode_attn: workspace %zu bytes < %zu for %d splits", workspace_bytes, need, S);
-    if ((long long)B * H_kv > 65535LL * 65535LL || B > 65535 || H_kv > 65535)
-        return fail(IE_ERR_UNSUPPORTED, "decode_attn: grid too large");
+    const long long nb_max = ((long long)max_context_len + block_size - 1) / block_size;
     ie::DecodeArgs a{};
     a.B = B; a.H_q = H_q; a.H_kv = H_kv; a.d = d;
     a.Q = Q; a.k_cache = k_cache; a.v_cache = v_cache; a.kv_dtype = kv_dtype;

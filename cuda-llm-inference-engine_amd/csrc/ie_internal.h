@@ -98,6 +98,16 @@ struct DecodeArgs {
     float* workspace;      // [B, H_q, num_splits, d + 2]
 };
 void launch_decode_attn(const DecodeArgs& a, hipStream_t s);
+// Host-side validation shared by ie_decode_attn and ie_decode_attn_noalloc
+// (capi.cpp): everything but the workspace; on IE_OK, *splits is the plan's
+// split count and *need_bytes its workspace size (0 when B == 0).
+int check_decode_attn(int B, int H_q, int H_kv, int d, const float* Q, const void* k_cache, const void* v_cache,
+                      int kv_dtype, const int* block_table, const int* context_lens, int max_context_len,
+                      int block_size, int num_blocks_per_seq, const float* O, int num_splits, size_t* need_bytes,
+                      int* splits);
+// Looks up (once per device) the address of ie_decode_attn_noalloc's scratch
+// array on the current device (decode_attn_noalloc.hip); called by ie_init.
+int decode_scratch_init();
 
 // Compute units of the current device (gemv_i8.hip).
 int num_cus();

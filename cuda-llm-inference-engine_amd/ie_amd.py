@@ -47,7 +47,9 @@ SIGNATURES = {
     "ie_topk": (_I, [_I, _P, _I, _I, _P, _P, _P]),
     "ie_top_k_draw": (_I, [_P, _P, _I, _F, ctypes.c_uint, _P]),
     "ie_check_token_ids": (_I, [_I, _P, _I]),
+    "ie_decode_attn_noalloc": (_I, [_I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P, _I, _P]),
 }
+DECODE_SCRATCH_BYTES = 32 << 20
 
 # include/ie_engine.h
 ENGINE_SIGNATURES = {
@@ -192,6 +194,21 @@ def decode_attn(Q, k_cache, v_cache, block_table, context_lens, max_ctx, block_s
     check("ie_decode_attn", B, H_q, H_kv, d, _ptr(Q), _ptr(k_cache), _ptr(v_cache), kv_dtype,
           _ptr(block_table), _ptr(context_lens), max_ctx, block_size, nbps, _ptr(out),
           _ptr(workspace), workspace.numel() * 4, splits, _stream(stream))
+    return out
+
+
+def decode_attn_noalloc(Q, k_cache, v_cache, block_table, context_lens, max_ctx, block_size, H_kv,
+                        kv_dtype=KV_F32, splits=0, out=None, stream=None):
+    """ie_decode_attn_noalloc: as decode_attn, split partials in the library's
+    per-device scratch (no workspace)."""
+    import torch
+
+    B, H_q, d = Q.shape
+    if out is None:
+        out = torch.empty_like(Q)
+    check("ie_decode_attn_noalloc", B, H_q, H_kv, d, _ptr(Q), _ptr(k_cache), _ptr(v_cache), kv_dtype,
+          _ptr(block_table), _ptr(context_lens), max_ctx, block_size, block_table.shape[1], _ptr(out),
+          splits, _stream(stream))
     return out
 
 

@@ -76,10 +76,11 @@ typedef enum { IE_KV_F32 = 0, IE_KV_BF16 = 1 } ie_kv_dtype;
 
 const char* ie_last_error(void);
 int ie_version(void);
-/* Optional: checks that the current device is gfx950 and makes the two small
+/* Optional: checks that the current device is gfx950, makes the two small
  * buffers of the compat samplers (sample_argmax / sample_top_k in
- * ie_compat.h), so nothing allocates afterwards; calling it first also keeps
- * the HIP runtime's one-time start-up out of timed regions. */
+ * ie_compat.h), so nothing allocates afterwards, and looks up the current
+ * device's address of ie_decode_attn_noalloc's scratch; calling it first also
+ * keeps the HIP runtime's one-time start-up out of timed regions. */
 int ie_init(void);
 
 /* Per-row symmetric quantizer: scales[r] = max|x_r|/127 (1 for a zero row),
@@ -123,6 +124,24 @@ int ie_decode_attn(int B, int H_q, int H_kv, int d, const float* Q,
                    int max_context_len, int block_size, int num_blocks_per_seq,
                    float* O, float* workspace, size_t workspace_bytes,
                    int num_splits, ie_stream_t stream);
+
+/* ie_decode_attn without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split partials go to a scratch array that the library holds on each GPU
+ * until the process ends: IE_DECODE_SCRATCH_BYTES, so B * H_q * splits *
+ * (d + 2) * 4 must fit (else IE_ERR_WORKSPACE, outputs untouched).  Nothing
+ * is allocated and the scratch needs no clearing (every split slot is written
+ * before the merge reads it), but all calls on one GPU share it: calls that
+ * overlap in time on that GPU (other streams, other host threads) race.
+ * Same kernels, split plan and results as ie_decode_attn. */
+#define IE_DECODE_SCRATCH_BYTES ((size_t)32 << 20)
+int ie_decode_attn_noalloc(int B, int H_q, int H_kv, int d, const float* Q,
+                           const void* k_cache, const void* v_cache,
+                           int kv_dtype, const int* block_table,
+                           const int* context_lens, int max_context_len,
+                           int block_size, int num_blocks_per_seq, float* O,
+                           int num_splits, ie_stream_t stream);
 
 /* Causal attention of a prompt chunk over the paged cache: P query tokens per
  * sequence, token t of sequence b at position start_pos + t, whose K/V (and

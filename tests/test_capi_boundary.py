@@ -16,7 +16,7 @@ COMPAT = os.path.join(ROOT, "include", "ie_compat.h")
 LIB = os.path.join(PKG, "libie_amd.so")
 
 
-SIGS_EXPECTED = 21  # entry points declared in include/ie_amd.h
+SIGS_EXPECTED = 22  # entry points declared in include/ie_amd.h
 
 
 def declared_c_functions(path=HDR):
@@ -200,3 +200,24 @@ int main() {
         r = subprocess.run([exe], capture_output=True, text=True)
         assert r.returncode == 0, (r.returncode, r.stderr)
         assert "rejected" in r.stderr
+
+
+def test_decode_attn_noalloc_rejects_plans_beyond_its_scratch(ie):
+    """ie_decode_attn_noalloc validates like ie_decode_attn, then refuses a
+    plan whose B * H_q * splits * (d + 2) * 4 bytes of partials exceed the
+    library's scratch (IE_ERR_WORKSPACE), all before any HIP call."""
+    n = None
+    B, H_q, H_kv, d, ctx, splits = 64, 32, 8, 128, 8192, 64
+    assert B * H_q * splits * (d + 2) * 4 > ie.DECODE_SCRATCH_BYTES
+    args = (B, H_q, H_kv, d, FAKE, FAKE, FAKE, 0, FAKE, FAKE, ctx, 16, ctx // 16, FAKE)
+    assert st(ie, "ie_decode_attn_noalloc", *args, splits, n) == ie.IE_ERR_WORKSPACE
+    assert "scratch" in ie.last_error()
+    # the same validation as ie_decode_attn: group size 3, head dim 96
+    assert st(ie, "ie_decode_attn_noalloc", 1, 12, 4, 64, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 16, 16, 1, FAKE, 0,
+              n) == ie.IE_ERR_UNSUPPORTED
+    assert st(ie, "ie_decode_attn_noalloc", 1, 4, 4, 96, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 16, 16, 1, FAKE, 0,
+              n) == ie.IE_ERR_UNSUPPORTED
+    assert st(ie, "ie_decode_attn_noalloc", 1, 4, 4, 64, n, FAKE, FAKE, 0, FAKE, FAKE, 16, 16, 1, FAKE, 0,
+              n) == ie.IE_ERR_INVALID
+    # B = 0 is a no-op
+    assert st(ie, "ie_decode_attn_noalloc", 0, 4, 4, 64, n, n, n, 0, n, n, 16, 16, 1, n, 0, n) == ie.IE_OK
