@@ -11,8 +11,9 @@ paged cache, max |diff| < 1e-5), and calls run_int8_gemm_bias /
 _bias_gelu / _bias_residual, run_layernorm, run_embedding,
 run_flash_attn_v2, sample_argmax and sample_top_k.  Here each output is
 checked against the oracle on the program's own inputs: quantizer, int32-exact
-GEMMs and embedding bit-exact, GELU 2e-6, attention 1e-5 absolute (the
-reference's bar), LayerNorm 1e-5 of scale, sampled ids equal.
+GEMMs and embedding bit-exact, GELU 2e-6 relative plus the tanhf bound
+stated in the test, attention 1e-5 absolute (the reference's bar), LayerNorm
+1e-5 of scale, sampled ids equal.
 """
 import os
 import subprocess
@@ -72,9 +73,18 @@ def test_int8_gemm_reference_cases(orc, run_dir):
         # the reference test's own acceptance bound against the fp32 GEMM
         ref = A.astype(np.float64) @ B.astype(np.float64)
         assert np.abs(C - ref).max() < 0.012 * np.sqrt(K), cs
-        assert np.array_equal(load(d, cs, "C_bias", np.float32, (M, N)), orc.gemm(Ap, Bp, sA, sB, 1, bias))
+        v = load(d, cs, "C_bias", np.float32, (M, N))
+        assert np.array_equal(v, orc.gemm(Ap, Bp, sA, sB, 1, bias))
+        # GELU: the device's and glibc's tanhf may differ by an ulp or two,
+        # and 0.5 v (1 + tanh u) carries that absolute error (<= 1.2e-7 at
+        # |tanh| near 1) times |v| / 2 into the output, whose relative error
+        # grows where 1 + tanh cancels (v well below 0).  Bar: 2e-6 relative
+        # plus 1.2e-7 |v|, with v the (bit-exact) BiasOnly output.
         gelu = load(d, cs, "C_gelu", np.float32, (M, N))
-        assert np.allclose(gelu, orc.gemm(Ap, Bp, sA, sB, 2, bias), rtol=2e-6, atol=1e-7), cs
+        want = orc.gemm(Ap, Bp, sA, sB, 2, bias)
+        err = np.abs(gelu.astype(np.float64) - want)
+        bound = 2e-6 * np.abs(want) + 1.2e-7 * np.abs(v)
+        assert (err <= bound).all(), (cs, float((err / bound).max()))
         assert np.array_equal(load(d, cs, "C_residual", np.float32, (M, N)),
                               orc.gemm(Ap, Bp, sA, sB, 3, bias, res)), cs
 
