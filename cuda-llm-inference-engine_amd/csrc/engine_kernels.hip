@@ -64,6 +64,28 @@ __global__ __launch_bounds__(256) void prefill_qkv_write_kernel(
     vc[slot * d + i] = to_kv<KV>(row[2 * d + i]);
 }
 
+// The fp32 comparison backend's epilogue after a vendor fp32 GEMM g [M, N]
+// (src/gpt2_engine.cu:349-390): bias, bias + tanh-GELU, or bias + residual,
+// in the reference's order of additions (C += bias + residual).  out may be
+// residual (the hidden state updated in place).
+__global__ __launch_bounds__(256) void fp32_epilogue_kernel(int M, int N, const float* __restrict__ g,
+                                                            const float* __restrict__ bias,
+                                                            const float* residual, float* out, int epi) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)M * N) return;
+    const int j = (int)(idx % (size_t)N);
+    const float c = g[idx];
+    if (epi == IE_EPI_BIAS_GELU) {
+        const float v = c + bias[j];
+        const float v3 = v * v * v;
+        out[idx] = 0.5f * v * (1.0f + tanhf(0.7978845608f * fmaf(0.044715f, v3, v)));
+    } else if (epi == IE_EPI_BIAS_RESIDUAL) {
+        out[idx] = c + (bias[j] + residual[idx]);
+    } else {
+        out[idx] = c + bias[j];
+    }
+}
+
 __global__ void set_positions_kernel(int B, int pos, int* __restrict__ positions, int* __restrict__ ctx_lens) {
     const int b = blockIdx.x * 64 + threadIdx.x;
     if (b < B) {
@@ -106,6 +128,13 @@ void launch_prefill_qkv_write(int B, int P, int start, int d, const float* qkv,
         prefill_qkv_write_kernel<float><<<blocks, 256, 0, s>>>(
             B, P, start, d, qkv, block_table, nbps, block_size, Q, static_cast<float*>(kc),
             static_cast<float*>(vc));
+}
+
+void launch_fp32_epilogue(int M, int N, const float* g, const float* bias, const float* residual, float* out,
+                          int epi, hipStream_t s) {
+    const size_t total = (size_t)M * N;
+    if (total == 0) return;
+    fp32_epilogue_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(M, N, g, bias, residual, out, epi);
 }
 
 void launch_set_positions(int B, int pos, int* positions, int* ctx_lens, hipStream_t s) {

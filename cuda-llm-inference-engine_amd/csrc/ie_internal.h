@@ -153,6 +153,10 @@ void launch_prefill_qkv_write(int B, int P, int start, int d, const float* qkv,
                               void* kc, void* vc, int kv_dtype, hipStream_t s);
 // positions[b] = ctx_lens[b] = pos for every sequence.
 void launch_set_positions(int B, int pos, int* positions, int* ctx_lens, hipStream_t s);
+// fp32 comparison backend: out = epilogue(g) for epi in {BIAS, BIAS_GELU,
+// BIAS_RESIDUAL}, g [M, N] the vendor GEMM's output (out may alias residual).
+void launch_fp32_epilogue(int M, int N, const float* g, const float* bias, const float* residual, float* out,
+                          int epi, hipStream_t s);
 
 // ---- support ops (support.hip) ----
 void launch_layernorm(int rows, int cols, const float* x, const float* g,

@@ -62,7 +62,7 @@ extern "C" {
 int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n_heads, int d_model,
                      int d_ff, int vocab_size, int max_seq_len, unsigned long long seed, int max_batch,
                      int kv_dtype, int int8_lm_head, int use_graph, int fuse, int prefill,
-                     int prefill_chunk) {
+                     int prefill_chunk, int backend) {
     if (!out) return ie::fail(IE_ERR_INVALID, "ie_engine_create: out is null");
     *out = nullptr;
     GPT2EngineOptions opt;
@@ -74,6 +74,9 @@ int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n
     opt.prefill = prefill != 0;
     opt.prefill_chunk = prefill_chunk;
     if (prefill_chunk < 0) return ie::fail(IE_ERR_INVALID, "ie_engine_create: prefill_chunk=%d", prefill_chunk);
+    if (backend != IE_BACKEND_INT8 && backend != IE_BACKEND_FP32)
+        return ie::fail(IE_ERR_INVALID, "ie_engine_create: backend=%d", backend);
+    opt.backend = backend == IE_BACKEND_FP32 ? InferenceBackend::CUBLAS_FP32 : InferenceBackend::CUSTOM_INT8;
     return guarded("ie_engine_create", [&] {
         GPT2Engine* e = model_dir ? new GPT2Engine(std::string(model_dir), opt)
                                   : new GPT2Engine(make_cfg(n_layers, n_heads, d_model, d_ff, vocab_size,

@@ -30,6 +30,7 @@
 #include <stdexcept>
 
 #include "../csrc/ie_internal.h"
+#include "vendor_blas.h"
 
 namespace {
 
@@ -153,11 +154,22 @@ struct HostModel {
         std::vector<float> ln1_g, ln1_b, ln2_g, ln2_b, qkv_b, out_b, up_b, down_b;
         std::vector<float> qkv_s, out_s, up_s, down_s;
         std::vector<int32_t> qkv_w, out_w, up_w, down_w;
+        // fp32 weights in the exporter's [K, N] layout (fp32 backend, writer)
+        std::vector<float> qkv_f, out_f, up_f, down_f;
     };
     std::vector<Layer> layers;
 };
 
-HostModel random_model(const GPT2Config& c, uint64_t seed) {
+// [rows, cols] -> [cols, rows]
+std::vector<float> transpose(const std::vector<float>& a, int rows, int cols) {
+    std::vector<float> t(a.size());
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) t[(size_t)c * rows + r] = a[(size_t)r * cols + c];
+    return t;
+}
+
+// keep_fp32: also keep each linear's fp32 weights as the exporter's [K, N].
+HostModel random_model(const GPT2Config& c, uint64_t seed, bool keep_fp32 = false) {
     validate(c);
     HostModel m;
     m.cfg = c;
@@ -169,25 +181,31 @@ HostModel random_model(const GPT2Config& c, uint64_t seed) {
     m.lnf_g.assign(d, 1.0f);
     m.lnf_b.assign(d, 0.0f);
     m.layers.resize(c.n_layers);
+    // weights drawn directly in the exporter's transposed [N=out, K=in] layout
+    auto linear = [&](int N, int K, std::vector<int32_t>& w, std::vector<float>& s, std::vector<float>& f) {
+        const std::vector<float> wt = nxt((size_t)N * K);
+        quantize_rows_host(wt, N, K, w, s);
+        if (keep_fp32) f = transpose(wt, N, K);
+    };
     for (auto& L : m.layers) {
         L.ln1_g.assign(d, 1.0f);
         L.ln1_b.assign(d, 0.0f);
         L.ln2_g.assign(d, 1.0f);
         L.ln2_b.assign(d, 0.0f);
-        // weights drawn directly in the exporter's transposed [N=out, K=in] layout
-        quantize_rows_host(nxt((size_t)3 * d * d), 3 * d, d, L.qkv_w, L.qkv_s);
+        linear(3 * d, d, L.qkv_w, L.qkv_s, L.qkv_f);
         L.qkv_b = nxt(3 * d);
-        quantize_rows_host(nxt((size_t)d * d), d, d, L.out_w, L.out_s);
+        linear(d, d, L.out_w, L.out_s, L.out_f);
         L.out_b = nxt(d);
-        quantize_rows_host(nxt((size_t)ff * d), ff, d, L.up_w, L.up_s);
+        linear(ff, d, L.up_w, L.up_s, L.up_f);
         L.up_b = nxt(ff);
-        quantize_rows_host(nxt((size_t)d * ff), d, ff, L.down_w, L.down_s);
+        linear(d, ff, L.down_w, L.down_s, L.down_f);
         L.down_b = nxt(d);
     }
     return m;
 }
 
-HostModel load_model(const std::string& dir) {
+// want_fp32: also read {name}_weight_fp32.bin [K, N] (python/export_gpt2.py:48-57).
+HostModel load_model(const std::string& dir, bool want_fp32 = false) {
     HostModel m;
     m.cfg = read_config(dir + "/config.json");
     const GPT2Config& c = m.cfg;
@@ -219,6 +237,12 @@ HostModel load_model(const std::string& dir) {
         L.down_w = read_bin<int32_t>(p + "ffn_down_weight.bin", (size_t)d * ff / 4);
         L.down_s = read_bin<float>(p + "ffn_down_scale.bin", d);
         L.down_b = read_bin<float>(p + "ffn_down_bias.bin", d);
+        if (want_fp32) {
+            L.qkv_f = read_bin<float>(p + "qkv_weight_fp32.bin", (size_t)d * 3 * d);
+            L.out_f = read_bin<float>(p + "out_weight_fp32.bin", (size_t)d * d);
+            L.up_f = read_bin<float>(p + "ffn_up_weight_fp32.bin", (size_t)d * ff);
+            L.down_f = read_bin<float>(p + "ffn_down_weight_fp32.bin", (size_t)ff * d);
+        }
     }
     return m;
 }
@@ -236,6 +260,7 @@ struct GPT2Engine::Impl {
     struct Layer {
         float *ln1_g, *ln1_b, *ln2_g, *ln2_b, *qkv_b, *out_b, *up_b, *down_b;
         QuantWeight qkv, out, up, down;
+        float *qkv_f = nullptr, *out_f = nullptr, *up_f = nullptr, *down_f = nullptr;  // fp32 backend
     };
     std::vector<Layer> layers;
     QuantWeight head{};  // INT8 LM head (quantized wte), optional
@@ -245,6 +270,10 @@ struct GPT2Engine::Impl {
     float *logits = nullptr;
     int32_t* act_q = nullptr;
     float* act_s = nullptr;
+    // fp32 backend: the vendor GEMM and its output rows [max_batch, max(3d, ff)]
+    bool fp32 = false;
+    std::unique_ptr<ie::VendorSgemm> blas;
+    float* gemm_out = nullptr;
 
     // paged KV cache: per layer [P, bs, H, dh]; row b of the block table maps
     // its nbps logical blocks to physical blocks b * nbps + i
@@ -278,6 +307,7 @@ struct GPT2Engine::Impl {
         float *x = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr;
         float* act_s = nullptr;
         int32_t* act_q = nullptr;
+        float* gemm_out = nullptr;  // fp32 backend
         int* ids = nullptr;  // pinned host mirror in host_ids
         int* host_ids = nullptr;
     } pf;
@@ -315,6 +345,16 @@ struct GPT2Engine::Impl {
         if (opt.kv_dtype != IE_KV_F32 && opt.kv_dtype != IE_KV_BF16) throw std::runtime_error("kv_dtype");
         HIPC(hipStreamCreate(&stream));
         const int d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size, B = opt.max_batch;
+        fp32 = opt.backend == InferenceBackend::CUBLAS_FP32;
+        if (fp32) {
+            for (const auto& L : m.layers)
+                if (L.qkv_f.empty() || L.out_f.empty() || L.up_f.empty() || L.down_f.empty())
+                    throw std::runtime_error("fp32 backend: the model has no fp32 weights");
+            blas.reset(new ie::VendorSgemm(stream));
+            // vendor library calls stay out of graph capture
+            opt.use_graph = false;
+            opt.fuse = false;
+        }
         wte = upload(m.wte);
         wpe = upload(m.wpe);
         lnf_g = upload(m.lnf_g);
@@ -333,6 +373,12 @@ struct GPT2Engine::Impl {
             D.up_b = upload(L.up_b);
             D.down = upload_q(L.down_w, L.down_s, d, ff);
             D.down_b = upload(L.down_b);
+            if (fp32) {
+                D.qkv_f = upload(L.qkv_f);
+                D.out_f = upload(L.out_f);
+                D.up_f = upload(L.up_f);
+                D.down_f = upload(L.down_f);
+            }
             layers.push_back(D);
         }
         if (opt.int8_lm_head) {
@@ -350,6 +396,7 @@ struct GPT2Engine::Impl {
         logits = dev<float>((size_t)B * V);
         act_q = dev<int32_t>((size_t)B * std::max(d, ff) / 4);
         act_s = dev<float>(B);
+        if (fp32) gemm_out = dev<float>((size_t)B * std::max(3 * d, ff));
 
         nbps = (cfg.max_seq_len + kBlock - 1) / kBlock;
         phys_blocks = B * nbps;
@@ -475,6 +522,24 @@ struct GPT2Engine::Impl {
         IEC(ie_argmax(B, logits, V, tokens, st));
     }
 
+    // One linear of the unfused step or of prefill over M rows:
+    // out = epilogue(in . W) as the INT8 path (the per-row activation
+    // quantizer, then the INT8 GEMM with its epilogue, through the C ABI) or,
+    // with the fp32 backend, a vendor fp32 GEMM on the [K, N] weights followed
+    // by the same epilogue in fp32 (src/gpt2_engine.cu:530-610).
+    void linear(int M, const QuantWeight& w, const float* wf, const float* in, int epi, const float* bias,
+                const float* res, float* out, int32_t* aq, float* as, float* gout) {
+        ie_stream_t st = (ie_stream_t)stream;
+        if (fp32) {
+            blas->rowmajor(M, w.N, w.K, in, wf, gout);
+            ie::launch_fp32_epilogue(M, w.N, gout, bias, res, out, epi, stream);
+            IEC(ie::check_launch("fp32 epilogue"));
+            return;
+        }
+        IEC(ie_quantize_fp32_to_int8(M, w.K, in, aq, as, st));
+        IEC(ie_int8_gemm(M, w.N, w.K, aq, w.packed, as, w.scale, epi, bias, res, out, st));
+    }
+
     void enqueue_step(int B) {
         if (fused)
             enqueue_step_fused(B);
@@ -486,32 +551,24 @@ struct GPT2Engine::Impl {
     // leaves logits, writes the argmax into tokens and advances positions.
     // Every operation goes through the public C ABI.
     void enqueue_step_unfused(int B) {
-        const int d = cfg.d_model, ff = cfg.d_ff, H = cfg.n_heads;
+        const int d = cfg.d_model, H = cfg.n_heads;
         hipStream_t s = stream;
         ie_stream_t st = (ie_stream_t)s;
         IEC(ie_embedding_batch(B, tokens, positions, d, wte, wpe, x, st));
         for (int l = 0; l < cfg.n_layers; ++l) {
             const Layer& L = layers[l];
             IEC(ie_layernorm(B, d, x, L.ln1_g, L.ln1_b, xn, 1e-5f, st));
-            IEC(ie_quantize_fp32_to_int8(B, d, xn, act_q, act_s, st));
-            IEC(ie_int8_gemm(B, 3 * d, d, act_q, L.qkv.packed, act_s, L.qkv.scale, IE_EPI_BIAS, L.qkv_b,
-                             nullptr, qkv, st));
+            linear(B, L.qkv, L.qkv_f, xn, IE_EPI_BIAS, L.qkv_b, nullptr, qkv, act_q, act_s, gemm_out);
             ie::launch_qkv_split_append(B, d, qkv, positions, block_table, nbps, kBlock, q, layer_k(l),
                                         layer_v(l), opt.kv_dtype, ctx_lens, s);
             IEC(ie::check_launch("qkv_split_append"));
             IEC(ie_decode_attn(B, H, H, cfg.d_head, q, layer_k(l), layer_v(l), opt.kv_dtype,
                                block_table, ctx_lens, plan.max_ctx, kBlock, nbps, attn, ws, ws_bytes, plan.splits,
                                st));
-            IEC(ie_quantize_fp32_to_int8(B, d, attn, act_q, act_s, st));
-            IEC(ie_int8_gemm(B, d, d, act_q, L.out.packed, act_s, L.out.scale, IE_EPI_BIAS_RESIDUAL,
-                             L.out_b, x, x, st));
+            linear(B, L.out, L.out_f, attn, IE_EPI_BIAS_RESIDUAL, L.out_b, x, x, act_q, act_s, gemm_out);
             IEC(ie_layernorm(B, d, x, L.ln2_g, L.ln2_b, xn, 1e-5f, st));
-            IEC(ie_quantize_fp32_to_int8(B, d, xn, act_q, act_s, st));
-            IEC(ie_int8_gemm(B, ff, d, act_q, L.up.packed, act_s, L.up.scale, IE_EPI_BIAS_GELU, L.up_b,
-                             nullptr, h, st));
-            IEC(ie_quantize_fp32_to_int8(B, ff, h, act_q, act_s, st));
-            IEC(ie_int8_gemm(B, d, ff, act_q, L.down.packed, act_s, L.down.scale, IE_EPI_BIAS_RESIDUAL,
-                             L.down_b, x, x, st));
+            linear(B, L.up, L.up_f, xn, IE_EPI_BIAS_GELU, L.up_b, nullptr, h, act_q, act_s, gemm_out);
+            linear(B, L.down, L.down_f, h, IE_EPI_BIAS_RESIDUAL, L.down_b, x, x, act_q, act_s, gemm_out);
         }
         enqueue_head(B);
         ie::launch_advance(B, positions, s);
@@ -610,6 +667,7 @@ struct GPT2Engine::Impl {
         pf.h = static_cast<float*>(alloc(R * ff * 4));
         pf.act_q = static_cast<int32_t*>(alloc(R * std::max(d, ff)));
         pf.act_s = static_cast<float*>(alloc(R * 4));
+        if (fp32) pf.gemm_out = static_cast<float*>(alloc(R * std::max(3 * d, ff) * 4));
         pf.ids = static_cast<int*>(alloc(R * 4));
         HIPC(hipHostMalloc(&pf.host_ids, R * sizeof(int)));
         pf.rows = rows;
@@ -631,7 +689,7 @@ struct GPT2Engine::Impl {
         if (!prefill_applies()) throw std::runtime_error("prefill needs d_head 64 or 128");
         if (pos + P > cfg.max_seq_len) throw std::runtime_error("prompt does not fit the context");
         check_ids(toks, (size_t)B * P);
-        const int d = cfg.d_model, ff = cfg.d_ff, H = cfg.n_heads, dh = cfg.d_head;
+        const int d = cfg.d_model, H = cfg.n_heads, dh = cfg.d_head;
         const int chunk = std::min(P, prefill_chunk(B));
         ensure_prefill(B * chunk);
         ie_stream_t st = (ie_stream_t)stream;
@@ -648,24 +706,20 @@ struct GPT2Engine::Impl {
             for (int l = 0; l < cfg.n_layers; ++l) {
                 const Layer& L = layers[l];
                 IEC(ie_layernorm(M, d, pf.x, L.ln1_g, L.ln1_b, pf.xn, 1e-5f, st));
-                IEC(ie_quantize_fp32_to_int8(M, d, pf.xn, pf.act_q, pf.act_s, st));
-                IEC(ie_int8_gemm(M, 3 * d, d, pf.act_q, L.qkv.packed, pf.act_s, L.qkv.scale, IE_EPI_BIAS, L.qkv_b,
-                                 nullptr, pf.qkv, st));
+                linear(M, L.qkv, L.qkv_f, pf.xn, IE_EPI_BIAS, L.qkv_b, nullptr, pf.qkv, pf.act_q, pf.act_s,
+                       pf.gemm_out);
                 ie::launch_prefill_qkv_write(B, Pc, pos, d, pf.qkv, block_table, nbps, kBlock, pf.q, layer_k(l),
                                              layer_v(l), opt.kv_dtype, stream);
                 IEC(ie::check_launch("prefill_qkv_write"));
                 IEC(ie_prefill_attn(B, Pc, H, H, dh, pf.q, layer_k(l), layer_v(l), opt.kv_dtype, block_table, nbps,
                                     kBlock, pos, pf.attn, st));
-                IEC(ie_quantize_fp32_to_int8(M, d, pf.attn, pf.act_q, pf.act_s, st));
-                IEC(ie_int8_gemm(M, d, d, pf.act_q, L.out.packed, pf.act_s, L.out.scale, IE_EPI_BIAS_RESIDUAL,
-                                 L.out_b, pf.x, pf.x, st));
+                linear(M, L.out, L.out_f, pf.attn, IE_EPI_BIAS_RESIDUAL, L.out_b, pf.x, pf.x, pf.act_q, pf.act_s,
+                       pf.gemm_out);
                 IEC(ie_layernorm(M, d, pf.x, L.ln2_g, L.ln2_b, pf.xn, 1e-5f, st));
-                IEC(ie_quantize_fp32_to_int8(M, d, pf.xn, pf.act_q, pf.act_s, st));
-                IEC(ie_int8_gemm(M, ff, d, pf.act_q, L.up.packed, pf.act_s, L.up.scale, IE_EPI_BIAS_GELU, L.up_b,
-                                 nullptr, pf.h, st));
-                IEC(ie_quantize_fp32_to_int8(M, ff, pf.h, pf.act_q, pf.act_s, st));
-                IEC(ie_int8_gemm(M, d, ff, pf.act_q, L.down.packed, pf.act_s, L.down.scale, IE_EPI_BIAS_RESIDUAL,
-                                 L.down_b, pf.x, pf.x, st));
+                linear(M, L.up, L.up_f, pf.xn, IE_EPI_BIAS_GELU, L.up_b, nullptr, pf.h, pf.act_q, pf.act_s,
+                       pf.gemm_out);
+                linear(M, L.down, L.down_f, pf.h, IE_EPI_BIAS_RESIDUAL, L.down_b, pf.x, pf.x, pf.act_q, pf.act_s,
+                       pf.gemm_out);
             }
             pos += Pc;
         }
@@ -695,8 +749,8 @@ struct GPT2Engine::Impl {
 
     double bytes_per_step(int B) const {
         const double d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size;
-        double w = cfg.n_layers * (3 * d * d + d * d + 2 * d * ff);          // int8 weights
-        w += cfg.n_layers * 4.0 * (3 * d + d + ff + d) * 2;                 // scales + biases
+        double w = cfg.n_layers * (3 * d * d + d * d + 2 * d * ff) * (fp32 ? 4.0 : 1.0);  // linear weights
+        w += cfg.n_layers * 4.0 * (3 * d + d + ff + d) * (fp32 ? 1 : 2);   // biases (+ scales)
         w += cfg.n_layers * 4.0 * 4 * d;                                      // LayerNorm
         w += opt.int8_lm_head ? V * d + 4 * V : 4.0 * V * d;                  // LM head
         const double kv = 2.0 * cfg.n_layers * (double)B * pos * d * (opt.kv_dtype == IE_KV_BF16 ? 2 : 4);
@@ -734,11 +788,17 @@ static float ms_since(Clock::time_point t) {
 }
 
 GPT2Engine::GPT2Engine(const std::string& model_dir, GPT2EngineOptions opt) : impl_(new Impl) {
-    impl_->init(load_model(model_dir), opt);
+    impl_->init(load_model(model_dir, opt.backend == InferenceBackend::CUBLAS_FP32), opt);
+}
+
+GPT2Engine::GPT2Engine(const std::string& model_dir, InferenceBackend backend) : impl_(new Impl) {
+    GPT2EngineOptions opt;
+    opt.backend = backend;
+    impl_->init(load_model(model_dir, backend == InferenceBackend::CUBLAS_FP32), opt);
 }
 
 GPT2Engine::GPT2Engine(const GPT2Config& cfg, uint64_t seed, GPT2EngineOptions opt) : impl_(new Impl) {
-    impl_->init(random_model(cfg, seed), opt);
+    impl_->init(random_model(cfg, seed, opt.backend == InferenceBackend::CUBLAS_FP32), opt);
 }
 
 GPT2Engine::~GPT2Engine() = default;
@@ -892,7 +952,7 @@ void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, in
 }
 
 void GPT2Engine::write_random_model(const std::string& dir, const GPT2Config& cfg, uint64_t seed) {
-    const HostModel m = random_model(cfg, seed);
+    const HostModel m = random_model(cfg, seed, true);
     ::mkdir(dir.c_str(), 0755);
     {
         std::ofstream f(dir + "/config.json");
@@ -928,5 +988,10 @@ void GPT2Engine::write_random_model(const std::string& dir, const GPT2Config& cf
         write_bin(p + "/ffn_down_weight.bin", L.down_w);
         write_bin(p + "/ffn_down_scale.bin", L.down_s);
         write_bin(p + "/ffn_down_bias.bin", L.down_b);
+        // python/export_gpt2.py:48-57: fp32 [K, N] for the vendor GEMM backend
+        write_bin(p + "/qkv_weight_fp32.bin", L.qkv_f);
+        write_bin(p + "/out_weight_fp32.bin", L.out_f);
+        write_bin(p + "/ffn_up_weight_fp32.bin", L.up_f);
+        write_bin(p + "/ffn_down_weight_fp32.bin", L.down_f);
     }
 }

@@ -16,6 +16,7 @@ IE_OK, IE_ERR_INVALID, IE_ERR_UNSUPPORTED, IE_ERR_WORKSPACE, IE_ERR_HIP = range(
 EPI_PLAIN, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESIDUAL, EPI_I32 = range(5)
 PATH_AUTO, PATH_GEMV, PATH_MFMA = range(3)
 KV_F32, KV_BF16 = 0, 1
+BACKEND_INT8, BACKEND_FP32 = 0, 1
 DA_REF_MAX_SPLITS = 16
 DA_MAX_SPLITS = 256
 
@@ -54,7 +55,7 @@ DECODE_SCRATCH_BYTES = 32 << 20
 # include/ie_engine.h
 ENGINE_SIGNATURES = {
     "ie_engine_create": (_I, [ctypes.POINTER(_P), ctypes.c_char_p, _I, _I, _I, _I, _I, _I,
-                              ctypes.c_ulonglong, _I, _I, _I, _I, _I, _I, _I]),
+                              ctypes.c_ulonglong, _I, _I, _I, _I, _I, _I, _I, _I]),
     "ie_engine_destroy": (_I, [_P]),
     "ie_engine_write_random_model": (_I, [ctypes.c_char_p, _I, _I, _I, _I, _I, _I, ctypes.c_ulonglong]),
     "ie_engine_reset": (_I, [_P]),
@@ -329,14 +330,15 @@ class Engine:
     random model of the given shape (GPT-2 Small by default)."""
 
     def __init__(self, model_dir=None, seed=0, max_batch=1, kv_dtype=KV_F32, int8_lm_head=False,
-                 use_graph=True, fuse=True, prefill=True, prefill_chunk=0, **cfg):
+                 use_graph=True, fuse=True, prefill=True, prefill_chunk=0, backend=BACKEND_INT8, **cfg):
         import numpy as np  # noqa: F401
 
         c = dict(GPT2_SMALL, **cfg)
         h = ctypes.c_void_p()
         check("ie_engine_create", ctypes.byref(h), None if model_dir is None else str(model_dir).encode(),
               c["n_layers"], c["n_heads"], c["d_model"], c["d_ff"], c["vocab_size"], c["max_seq_len"], seed,
-              max_batch, kv_dtype, int(int8_lm_head), int(use_graph), int(fuse), int(prefill), prefill_chunk)
+              max_batch, kv_dtype, int(int8_lm_head), int(use_graph), int(fuse), int(prefill), prefill_chunk,
+              backend)
         self.h = h
         v = (ctypes.c_int * 7)()
         check("ie_engine_config", h, ctypes.cast(v, ctypes.c_void_p))

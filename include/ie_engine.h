@@ -18,6 +18,10 @@ extern "C" {
 
 typedef struct ie_engine ie_engine;
 
+/* Backends (InferenceBackend in ie_gpt2_engine.h). */
+#define IE_BACKEND_INT8 0 /* the INT8 decode hot path (reference CUSTOM_INT8) */
+#define IE_BACKEND_FP32 1 /* vendor fp32 GEMMs (reference CUBLAS_FP32) */
+
 /* InferenceMetrics without its `generating` flag. */
 typedef struct {
     float ttft_ms, tpot_ms, itl_min_ms, itl_max_ms, itl_p95_ms, tps;
@@ -27,13 +31,13 @@ typedef struct {
 
 /* model_dir != NULL loads the reference on-disk format and ignores the
  * shape arguments; model_dir == NULL builds a random model of that shape.
- * fuse selects the fused decode step, prefill / prefill_chunk the prompt path
- * (GPT2EngineOptions). */
+ * fuse selects the fused decode step, prefill / prefill_chunk the prompt path,
+ * backend IE_BACKEND_INT8 or IE_BACKEND_FP32 (GPT2EngineOptions). */
 int ie_engine_create(ie_engine** out, const char* model_dir, int n_layers, int n_heads,
                      int d_model, int d_ff, int vocab_size, int max_seq_len,
                      unsigned long long seed, int max_batch, int kv_dtype,
                      int int8_lm_head, int use_graph, int fuse, int prefill,
-                     int prefill_chunk);
+                     int prefill_chunk, int backend);
 int ie_engine_destroy(ie_engine* e);
 int ie_engine_write_random_model(const char* dir, int n_layers, int n_heads, int d_model,
                                  int d_ff, int vocab_size, int max_seq_len,

@@ -64,6 +64,14 @@ struct InferenceMetrics {
     bool generating;
 };
 
+/* include/gpt2_types.cuh:43.  CUBLAS_FP32 keeps the reference's enumerator
+ * name so its callers compile unchanged; here that backend runs the four
+ * linears as vendor fp32 GEMMs (rocBLAS sgemm on the exporter's
+ * {name}_weight_fp32.bin [K, N] weights, src/gpt2_engine.cu:530-610) with
+ * this library's LayerNorm, paged KV cache, decode attention and LM head:
+ * the reference's fp32 comparison point for the INT8 path. */
+enum class InferenceBackend { CUSTOM_INT8, CUBLAS_FP32 };
+
 struct GPT2EngineOptions {
     int max_batch = 1;          /* sequences decoded together */
     int kv_dtype = IE_KV_F32;   /* IE_KV_F32 (reference) or IE_KV_BF16 */
@@ -78,12 +86,17 @@ struct GPT2EngineOptions {
      * when false, one decode step per prompt position). */
     bool prefill = true;
     int prefill_chunk = 0; /* tokens per sequence per prefill pass; 0 = 4096 / batch */
+    /* CUBLAS_FP32: vendor fp32 GEMMs (needs the fp32 weight files, or a
+     * random model); runs the unfused step without graph capture. */
+    InferenceBackend backend = InferenceBackend::CUSTOM_INT8;
 };
 
 class GPT2Engine {
 public:
     /* Loads a model directory in the reference format. */
     explicit GPT2Engine(const std::string& model_dir, GPT2EngineOptions opt = {});
+    /* The reference's constructor (src/gpt2_engine.cuh:11-12). */
+    GPT2Engine(const std::string& model_dir, InferenceBackend backend);
     /* Random-initialised model (weights and biases N(0, 0.02), LayerNorm
      * gamma 1, beta 0), quantized per row exactly as the exporter does. */
     GPT2Engine(const GPT2Config& cfg, uint64_t seed, GPT2EngineOptions opt = {});
@@ -122,7 +135,9 @@ public:
      * current context) for `batch` sequences; used for MBU. */
     double step_bytes(int batch) const;
 
-    /* Writes a random-initialised model in the reference's on-disk format. */
+    /* Writes a random-initialised model in the reference's on-disk format,
+     * with the exporter's fp32 [K, N] copies of the linear weights
+     * ({name}_weight_fp32.bin, python/export_gpt2.py:48-57). */
     static void write_random_model(const std::string& dir, const GPT2Config& cfg, uint64_t seed);
 
     struct Impl;

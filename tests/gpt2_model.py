@@ -105,13 +105,15 @@ class TorchRefGPT2:
       logits = LN_f(x) wte^T      (or the INT8 head: Lin over quantized wte)
     where Lin_w(a) = (int8(a) . int8(W)) * s_a * s_w + bias, int8() being the
     per-row symmetric quantizer applied to the fp32 rounding of `a`.  All other
-    arithmetic is float64.  `min_margin` records the smallest distance (in
+    arithmetic is float64.  With quantized=False the linears are plain
+    float64 x @ W + b on the exporter's fp32 [K, N] weights (the reference's
+    fp32 cuBLAS backend, src/gpt2_engine.cu:530-610).  `min_margin` records the smallest distance (in
     quantization steps) of any quantizer input from a rounding boundary:
     float32-level differences between two implementations cannot change a
     quantized value while it stays above ~1e-4.
     """
 
-    def __init__(self, path, batch=1, int8_lm_head=False, kv_bf16=False):
+    def __init__(self, path, batch=1, int8_lm_head=False, kv_bf16=False, quantized=True):
         import torch
 
         self.torch = torch
@@ -125,10 +127,12 @@ class TorchRefGPT2:
             return torch.from_numpy(a).double()
 
         def q(p, name, N, K):
+            b = f(f"{p}/{name}_bias.bin", (N,))
+            if not quantized:  # the exporter's fp32 [K, N] weights
+                return (f(f"{p}/{name}_weight_fp32.bin", (K, N)), b)
             w = np.fromfile(os.path.join(path, p, f"{name}_weight.bin"), np.int8).reshape(N, K)
             s = np.fromfile(os.path.join(path, p, f"{name}_scale.bin"), np.float32)
-            return (torch.from_numpy(w.astype(np.int64)), torch.from_numpy(s).double(),
-                    f(f"{p}/{name}_bias.bin", (N,)))
+            return (torch.from_numpy(w.astype(np.int64)), torch.from_numpy(s).double(), b)
 
         self.wte = f("wte.bin", (V, d))
         self.wpe = f("wpe.bin", (S, d))
@@ -167,6 +171,8 @@ class TorchRefGPT2:
         return qv, scale.double()
 
     def lin(self, a, w):
+        if len(w) == 2:  # unquantized: x @ W + b in float64
+            return a @ w[0] + w[1][None, :]
         qa, sa = self.quant(a)
         wq, ws, b = w
         return (qa @ wq.T).double() * sa[:, None] * ws[None, :] + b[None, :]

@@ -58,9 +58,11 @@ def test_engine_c_api_rejects_bad_arguments_without_a_gpu(ie):
     assert lib.ie_engine_generate(None, 1, 4, ctypes.cast(toks, P), 2, 0, None, None) == ie.IE_ERR_INVALID
     h = P()
     # negative prefill chunk
-    st = lib.ie_engine_create(ctypes.byref(h), None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, -5)
+    st = lib.ie_engine_create(ctypes.byref(h), None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, -5, 0)
     assert st == ie.IE_ERR_INVALID and "prefill_chunk" in ie.last_error()
-    assert lib.ie_engine_create(None, None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, 0) == ie.IE_ERR_INVALID
+    st = lib.ie_engine_create(ctypes.byref(h), None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, 0, 7)
+    assert st == ie.IE_ERR_INVALID and "backend" in ie.last_error()
+    assert lib.ie_engine_create(None, None, 2, 2, 128, 512, 1000, 64, 1, 1, 0, 0, 1, 1, 1, 0, 0) == ie.IE_ERR_INVALID
 
 
 def test_token_id_check_rejects_out_of_range(ie):
@@ -79,3 +81,28 @@ def test_token_id_check_rejects_out_of_range(ie):
     assert ie.call("ie_check_token_ids", 0, None, V) == ie.IE_OK
     assert ie.call("ie_check_token_ids", 2, None, V) == ie.IE_ERR_INVALID
     assert ie.call("ie_check_token_ids", 1, ctypes.cast(ok, ctypes.c_void_p), 0) == ie.IE_ERR_INVALID
+
+
+def test_writer_quantizer_and_fp32_files_pinned(ie, orc, tmp_path):
+    """The writer's quantizer (quantize_rows_host, the closed form of
+    python/export_gpt2.py:10-40) against the oracle's quantizer and a numpy
+    restatement of the exporter, bit for bit, on the fp32 weights the writer
+    also saves as {name}_weight_fp32.bin [K, N] (export_gpt2.py:48-57):
+    transposed to [N, K], quantized per output row, they give exactly the
+    int8 words and scales in {name}_weight.bin / _scale.bin."""
+    from gpt2_model import quantize_per_row
+
+    ie.write_random_model(tmp_path, seed=8, **TINY)
+    d, ff = TINY["d_model"], TINY["d_ff"]
+    for layer in ("layer_00", "layer_01"):
+        for name, K, N in [("qkv", d, 3 * d), ("out", d, d), ("ffn_up", d, ff), ("ffn_down", ff, d)]:
+            p = tmp_path / layer
+            wf = np.fromfile(p / f"{name}_weight_fp32.bin", dtype=np.float32)
+            assert wf.size == K * N
+            wt = np.ascontiguousarray(wf.reshape(K, N).T)
+            packed = np.fromfile(p / f"{name}_weight.bin", dtype=np.int32).reshape(N, K // 4)
+            scale = np.fromfile(p / f"{name}_scale.bin", dtype=np.float32)
+            op, os_ = orc.quantize(wt)
+            assert np.array_equal(packed, op) and np.array_equal(scale, os_), (layer, name)
+            npk, nps = quantize_per_row(wt)
+            assert np.array_equal(packed, npk) and np.array_equal(scale, nps), (layer, name)
