@@ -3,25 +3,37 @@
 
 Headline (`value`): INT8 GEMM throughput at M=N=K=8192 (Plain epilogue, int32
 accumulate, fp32 out) in TOP/s, one "step" = one GEMM launch over resident
-inputs.  The same JSON line carries:
-  roofline      the 8192^3 kernel against the dense i8 MFMA peak (5.0 POP/s)
+inputs.  Its operands are made (and quantized, untimed) first; the warm-up and
+timed launches run after the other GPU legs, so the part's clock has left its
+idle state (back-to-back launches on a just-woken GPU run up to ~20% slower
+for the first ~30).  The same JSON line carries:
+  roofline      the 8192^3 kernel against the dense i8 MFMA peak (5.0 POP/s);
+                mfma_util from a SQ_VALU_MFMA_BUSY_CYCLES / GRBM_GUI_ACTIVE pass
   vendor_gemm   hipBLASLt (torch._int_mm) on the same operands, same box
   gemv          decode-M (1, 4, 16) GEMMs on the GPT-2 weight shapes, the LM
-                head shape and 8192x8192, in GB/s of algorithmic bytes against
-                HBM (8 TB/s), weights rotated through >= 1 GiB of copies so the
-                256 MiB MALL cannot serve them
+                head shape, 8192x8192 and 8192x28672, in GB/s of algorithmic
+                bytes against HBM (8 TB/s), weights rotated through >= 1 GiB
+                of copies so the 256 MiB MALL cannot serve them;
+                gemv_roofline leads with BASELINE's M=1 K=N=8192
   gemm_m512     the GPT-2 shapes at M = 512 (prefill-sized), TOP/s
-  decode_attn   split-K paged decode attention, BASELINE cfg3 (MHA) and cfg4
-                (GQA, ctx 4096/8192/32768, fp32 and bf16 KV), GB/s of
-                algorithmic bytes against HBM
-  e2e_gpt2      GPT-2 Small decode tok/s (BASELINE cfg5), batch 1 and 16
+  ref_shapes    the reference's own bench shapes (INT8 GEMM 256^3..2048^3,
+                incl. BASELINE cfg1 512^3; its eight decode-attention
+                configurations) beside its published GTX 1650 Ti times
+  decode_attn   split-K paged decode attention, BASELINE cfg3 (MHA), cfg4
+                (GQA, ctx 4096/8192/32768, fp32 and bf16 KV) and G = 8 at
+                d = 128, GB/s of algorithmic bytes against HBM
+  e2e_gpt2      GPT-2 Small decode tok/s (BASELINE cfg5), batch 1 and 16, INT8
+                and the fp32 vendor-GEMM comparison backend
   sampler       top-k sampling: device selection kernel, one sample_top_k
                 call, the reference's whole-row copy, sampled decode at batch 1
   cpu_baseline  the C oracle (oracle/liborc.so) on a bounded sample of the
                 8192^3 GEMM, on this host's cores; cpu_baseline_attn the same
-                for decode attention cfg4 ctx 8192 fp32
-  traffic       HBM bytes per launch of the dominant kernels (rocprofv3
-                FETCH_SIZE / WRITE_SIZE passes, calibrated on a 1 GiB copy)
+                for decode attention cfg4 ctx 8192 fp32; cpu_baseline_detail
+                1-thread and all-thread figures for cfg1, the GPT-2 shapes at
+                M = 1/4/16, cfg3 and cfg4 at ctx 4096/8192, with the CPU model
+  traffic       HBM bytes per launch of the dominant kernels and the BASELINE
+                GEMV shapes (rocprofv3 FETCH_SIZE / WRITE_SIZE passes,
+                calibrated on a 1 GiB copy)
 Kernel durations come from HIP events on the stream the kernels run on.
 """
 import argparse
@@ -50,14 +62,13 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # The first ~30 back-to-back 8192^3 launches run up to ~20% slower than the
-    # steady state (measured 1772 TOP/s over launches 4-13, 2160 from ~36 on),
-    # so the default warm-up is 50 launches (~30 ms).
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--skip", default="", help="comma list of vendor,gemv,gemm512,attn,cpu,e2e,sampler")
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--skip", default="",
+                    help="comma list of vendor,gemv,gemm512,ref,attn,cpu,e2e,sampler,mfma")
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE passes")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--mfma-child", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
 
 
@@ -118,12 +129,12 @@ def gemm_bytes(M, N, K, bias=False, residual=False):
 
 
 # ------------------------------------------------------------------ headline
-def bench_headline(ie, steps, warmup):
+def headline_inputs(ie):
+    """BASELINE recipe: A, B fp32 ~ N(0,1) from a seed; A quantized per row and
+    B per column (= per row of B^T) with the library's quantizer (untimed)."""
     import torch
 
     M = N = K = 8192
-    # BASELINE recipe: A, B fp32 ~ N(0,1) from a seed; A quantized per row and
-    # B per column (= per row of B^T) with the library's quantizer (untimed).
     g = torch.Generator(device="cuda").manual_seed(42)
     Af = torch.randn((M, K), device="cuda", generator=g)
     Ap, sA = ie.quantize(Af)
@@ -132,6 +143,15 @@ def bench_headline(ie, steps, warmup):
     Bp, sB = ie.quantize(BTf)
     del BTf
     torch.cuda.empty_cache()
+    torch.cuda.synchronize()
+    return (Ap, Bp, sA, sB)
+
+
+def bench_headline(ie, inputs, steps, warmup):
+    import torch
+
+    M = N = K = 8192
+    Ap, Bp, sA, sB = inputs
     C = torch.empty((M, N), dtype=torch.float32, device="cuda")
 
     def launch():
@@ -153,7 +173,6 @@ def bench_headline(ie, steps, warmup):
         "kernel_ms": kern_ms,
         "kernel_tops": ops / (kern_ms * 1e-3) / 1e12,
         "bytes": gemm_bytes(M, N, K),
-        "inputs": (Ap, Bp, sA, sB),
     }
 
 
@@ -235,7 +254,7 @@ def bench_gemm512(ie):
 
 
 # ------------------------------------------------------------------ attention
-def attn_case(ie, B, H_q, H_kv, d, ctx, kv_bf16, uniform, seed):
+def attn_case(ie, B, H_q, H_kv, d, ctx, kv_bf16, uniform, seed, max_copies=64):
     import torch
 
     gen = torch.Generator().manual_seed(seed)
@@ -252,6 +271,7 @@ def attn_case(ie, B, H_q, H_kv, d, ctx, kv_bf16, uniform, seed):
     kv_bytes = int(lens.sum()) * H_kv * d * 2 * esz
     alg = kv_bytes + 2 * B * H_q * d * 4 + 4 * P + 4 * B
     copies = max(1, -(-(2 * ROTATE_BYTES) // max(kv_bytes, 1))) if kv_bytes < ROTATE_BYTES else 1
+    copies = min(copies, max_copies)
     gcuda = torch.Generator(device="cuda").manual_seed(seed)
     caches = []
     for _ in range(copies):
@@ -289,12 +309,49 @@ def attn_case(ie, B, H_q, H_kv, d, ctx, kv_bf16, uniform, seed):
     torch.cuda.empty_cache()
     return res
 
-
 def bench_attn(ie):
     out = [attn_case(ie, 8, 12, 12, 64, 1024, False, True, 3)]
     for ctx in (4096, 8192, 32768):
         for bf in (False, True):
             out.append(attn_case(ie, 32, 32, 8, 128, ctx, bf, False, ctx + bf))
+    # G = 8 at d = 128 (64 query heads over 8 KV heads), ctx 8192
+    for bf in (False, True):
+        out.append(attn_case(ie, 32, 64, 8, 128, 8192, bf, False, 88 + bf))
+    return out
+
+
+# ------------------------------------------------------------------ reference bench shapes
+# The reference's own benchmark shapes and its published times on a GTX 1650 Ti
+# (README.md:162-169, 183-186; benchmarks/int8_gemm_bench.cu:27,
+# benchmarks/decode_attention_bench.cu:57-67): context only, other hardware.
+REF_GEMM_US = {256: 23.7, 512: 93.2, 1024: 788.3, 2048: 5213.2}
+REF_ATTN_US = [((1, 8, 8, 128), 31.9), ((1, 8, 8, 256), 25.2), ((1, 8, 8, 512), 29.5), ((1, 8, 8, 1024), 51.8),
+               ((4, 8, 8, 256), 49.0), ((8, 8, 8, 512), 162.6), ((1, 16, 4, 256), 34.9), ((1, 32, 8, 512), 81.5)]
+
+
+def bench_ref_shapes(ie):
+    """INT8 GEMM S^3 (U(-1,1) operands quantized by the library, Plain
+    epilogue; 512^3 is BASELINE cfg1) and decode attention (d 64, block 16,
+    fp32, every sequence at ctx), timed from HIP graphs."""
+    import torch
+
+    out = {"gemm": [], "decode_attn": [], "reference_hw": "GTX 1650 Ti (README.md:28-30)"}
+    g = torch.Generator(device="cuda").manual_seed(11)
+    for S, ref_us in REF_GEMM_US.items():
+        A = torch.rand((S, S), device="cuda", generator=g) * 2 - 1
+        BT = torch.rand((S, S), device="cuda", generator=g) * 2 - 1
+        Ap, sA = ie.quantize(A)
+        Bp, sB = ie.quantize(BT)
+        C = torch.empty((S, S), device="cuda")
+        ms = graph_time(lambda i: ie.int8_gemm(Ap, Bp, sA, sB, ie.EPI_PLAIN, out=C), 20)
+        r = {"M=N=K": S, "us": round(ms * 1e3, 2), "TOPs": round(2.0 * S ** 3 / (ms * 1e-3) / 1e12, 2),
+             "reference_us": ref_us}
+        out["gemm"].append(r)
+        log(f"ref gemm {r}")
+    for (B, H_q, H_kv, ctx), ref_us in REF_ATTN_US:
+        r = attn_case(ie, B, H_q, H_kv, 64, ctx, False, True, ctx + B + H_q, max_copies=16)
+        out["decode_attn"].append({"B": B, "H_q": H_q, "H_kv": H_kv, "ctx": ctx, "us": r["us"], "GBps": r["GBps"],
+                                   "reference_us": ref_us})
     return out
 
 
@@ -311,15 +368,17 @@ def bench_e2e(ie):
     out = []
     rng = np.random.default_rng(128)
     # fused step (5 launches per layer) for both LM heads; the unfused step
-    # (every operation through the public C ABI) for comparison
-    for head_i8, fuse in ((False, True), (True, True), (False, False)):
-        eng = ie.Engine(None, seed=1234, max_batch=16, int8_lm_head=head_i8, fuse=fuse)
+    # (every operation through the public C ABI) and the fp32 vendor-GEMM
+    # backend (the reference's CUBLAS_FP32 comparison point) for comparison
+    for head_i8, fuse, backend in ((False, True, 0), (True, True, 0), (False, False, 0), (False, False, 1)):
+        eng = ie.Engine(None, seed=1234, max_batch=16, int8_lm_head=head_i8, fuse=fuse, backend=backend)
         for B in (1, 16):
             prompts = rng.integers(0, 50257, (B, 128)).astype(np.int32)
             eng.generate(prompts, 8, ignore_eos=True)  # warm up (graph capture)
             toks, m = eng.generate(prompts, 256, ignore_eos=True)
+            step = "fp32 vendor GEMM backend" if backend else "fused" if fuse else "unfused"
             r = {"batch": B, "lm_head": "int8" if head_i8 else "fp32 (reference)",
-                 "step": "fused" if fuse else "unfused", "prompt": "prefill",
+                 "step": step, "prompt": "prefill",
                  "decode_tok_s": round(m["tps"], 1), "tpot_ms": round(m["tpot_ms"], 4),
                  "ttft_ms": round(m["ttft_ms"], 2), "itl_p95_ms": round(m["itl_p95_ms"], 4),
                  "mbu": round(m["mbu"], 4), "tokens": int((toks >= 0).sum())}
@@ -396,14 +455,20 @@ def bench_sampler(ie):
 
 # ------------------------------------------------------------------ HBM traffic
 CALIB_BYTES = 1 << 30
-TRAFFIC_KERNELS = {"gemm": "gemm_i8_256_kernel", "gemv": "gemv_i8_parted_kernel",
-                   "attn": "decode_attn_balanced_kernel"}
+# Workloads of the FETCH_SIZE / WRITE_SIZE passes, in launch order: label,
+# kernel-name pattern, and for GEMVs (M, K, N).  A label's dispatches are the
+# pattern's matches in launch order (one per GEMV and attention label; the
+# headline GEMM's three launches are averaged).
+TRAFFIC_GEMV = [("gemv_8192_m1", 1, 8192, 8192), ("gemv_8192_m16", 16, 8192, 8192),
+                ("gemv_head_m1", 1, 768, 50257), ("gemv_head_m16", 16, 768, 50257),
+                ("gemv_28672_m1", 1, 8192, 28672)]
 
 
 def pmc_child(ie):
     """Workload profiled by the FETCH_SIZE / WRITE_SIZE passes: a 1 GiB device
-    copy (calibration: known bytes each way), then one launch of each dominant
-    kernel on its bench shape."""
+    copy (calibration: known bytes each way), three headline GEMM launches,
+    one launch per TRAFFIC_GEMV shape (fresh weights) and one cfg4 ctx 8192
+    fp32 attention call."""
     import torch
 
     src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device="cuda")
@@ -411,25 +476,27 @@ def pmc_child(ie):
     dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    h = bench_headline(ie, 2, 1)
+    h = bench_headline(ie, headline_inputs(ie), 2, 1)
     del h
+    torch.cuda.empty_cache()
     g = torch.Generator(device="cuda").manual_seed(9)
-    K, N = 8192, 28672
-    W = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
-    A = torch.randint(-127, 128, (1, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
-    sA = torch.ones(1, device="cuda")
-    sB = torch.ones(N, device="cuda")
-    ie.int8_gemm(A, W, sA, sB, ie.EPI_PLAIN)
-    torch.cuda.synchronize()
-    del W
-    attn_case(ie, 32, 32, 8, 128, 8192, False, False, 8192)
+    for _, M, K, N in TRAFFIC_GEMV:
+        W = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
+        A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
+        sA = torch.ones(M, device="cuda")
+        sB = torch.ones(N, device="cuda")
+        C = torch.empty((M, N), device="cuda")
+        torch.cuda.synchronize()
+        ie.int8_gemm(A, W, sA, sB, ie.EPI_PLAIN, out=C)
+        torch.cuda.synchronize()
+        del W
+    attn_case(ie, 32, 32, 8, 128, 8192, False, False, 8192, max_copies=1)
     torch.cuda.synchronize()
 
 
-def measure_traffic():
-    """Runs the PMC passes in child processes; returns per-kernel HBM bytes per
-    launch (FETCH_SIZE + WRITE_SIZE, KiB, scaled by what the counters read for
-    the calibration copy) or None if rocprofv3 is unavailable."""
+def _pmc_rows(counters, child_flag, extra=()):
+    """Runs this script as child_flag under rocprofv3 --pmc counters; returns
+    the counter rows (dicts) in dispatch order, or None."""
     import csv
     import shutil
     import subprocess
@@ -437,33 +504,56 @@ def measure_traffic():
 
     if shutil.which("rocprofv3") is None:
         return None
-    out = {}
     with tempfile.TemporaryDirectory(dir="/tmp") as td:
-        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            d = os.path.join(td, counter)
-            cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv",
-                   "-d", d, "-o", "run", "--", sys.executable, os.path.abspath(__file__), "--pmc-child"]
-            r = subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), capture_output=True,
-                               text=True)
-            files = [os.path.join(dp, f) for dp, _, fs in os.walk(d) for f in fs
-                     if f.endswith("counter_collection.csv")]
-            if r.returncode != 0 and not files:
-                log(f"traffic pass {counter} failed rc={r.returncode}: {r.stderr[-500:]}")
-                return None
-            vals = {}
-            for row in csv.DictReader(open(files[0])):
-                if row["Counter_Name"] != counter:
-                    continue
-                name = row["Kernel_Name"]
-                key = "copy" if "copy" in name.lower() or "elementwise_kernel" in name else None
-                for k, pat in TRAFFIC_KERNELS.items():
-                    if pat in name:
-                        key = k
-                if key:
-                    vals.setdefault(key, []).append(float(row["Counter_Value"]) * 1024.0)
-            for k, v in vals.items():
-                # the calibration copy is the largest "copy"-like dispatch
-                out.setdefault(k, {})[counter] = max(v) if k == "copy" else sum(v) / len(v)
+        cmd = ["timeout", "-s", "KILL", "150", "rocprofv3", "--pmc", *counters, *extra, "--output-format", "csv",
+               "-d", td, "-o", "run", "--", sys.executable, os.path.abspath(__file__), child_flag]
+        r = subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), capture_output=True, text=True)
+        found = {}
+        for dp, _, fs in os.walk(td):
+            for f in fs:
+                if f.endswith(".csv"):
+                    found[f] = os.path.join(dp, f)
+        cc = [v for k, v in found.items() if k.endswith("counter_collection.csv")]
+        if not cc:
+            log(f"pmc pass {counters} failed rc={r.returncode}: {r.stderr[-500:]}")
+            return None
+        rows = list(csv.DictReader(open(cc[0])))
+        kt = [v for k, v in found.items() if k.endswith("kernel_trace.csv")]
+        trace = list(csv.DictReader(open(kt[0]))) if kt else []
+    key = "Dispatch_Id" if rows and "Dispatch_Id" in rows[0] else None
+    if key:
+        rows.sort(key=lambda x: int(x[key]))
+        trace.sort(key=lambda x: int(x.get(key, 0) or 0))
+    return rows, trace
+
+
+def measure_traffic():
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, KiB per dispatch, scaled
+    by what the counters read for the 1 GiB calibration copy), per label."""
+    out = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        got = _pmc_rows([counter], "--pmc-child")
+        if got is None:
+            return None
+        vals = {}
+        gemv_i = 0
+        for row in got[0]:
+            if row["Counter_Name"] != counter:
+                continue
+            name, v = row["Kernel_Name"], float(row["Counter_Value"]) * 1024.0
+            if "copy" in name.lower() or "elementwise_kernel" in name:
+                vals["copy"] = max(vals.get("copy", 0.0), v)
+            elif "gemm_i8_256_kernel" in name:
+                vals.setdefault("gemm", []).append(v)
+            elif "gemv_i8_" in name and gemv_i < len(TRAFFIC_GEMV):
+                vals[TRAFFIC_GEMV[gemv_i][0]] = v
+                gemv_i += 1
+            elif "decode_attn_balanced_kernel" in name:
+                vals["attn"] = v
+        if "gemm" in vals:
+            vals["gemm"] = sum(vals["gemm"]) / len(vals["gemm"])
+        for k, v in vals.items():
+            out.setdefault(k, {})[counter] = v
     cp = out.get("copy", {})
     if not cp.get("FETCH_SIZE") or not cp.get("WRITE_SIZE"):
         return None
@@ -471,11 +561,62 @@ def measure_traffic():
     w_scale = CALIB_BYTES / cp["WRITE_SIZE"]
     res = {"calibration": {"copy_bytes": CALIB_BYTES, "fetch_factor": round(f_scale, 4),
                            "write_factor": round(w_scale, 4)}}
-    for k in TRAFFIC_KERNELS:
-        if k in out and "FETCH_SIZE" in out[k] and "WRITE_SIZE" in out[k]:
-            res[k] = {"fetch_bytes": int(out[k]["FETCH_SIZE"] * f_scale),
-                      "write_bytes": int(out[k]["WRITE_SIZE"] * w_scale)}
+    alg = {lbl: gemm_bytes(M, N, K) for lbl, M, K, N in TRAFFIC_GEMV}
+    alg["gemm"] = gemm_bytes(8192, 8192, 8192)
+    for k, v in out.items():
+        if k != "copy" and "FETCH_SIZE" in v and "WRITE_SIZE" in v:
+            fb, wb = int(v["FETCH_SIZE"] * f_scale), int(v["WRITE_SIZE"] * w_scale)
+            res[k] = {"fetch_bytes": fb, "write_bytes": wb}
+            if k in alg:
+                res[k]["algorithmic_bytes"] = alg[k]
+                res[k]["traffic_over_algorithmic"] = round((fb + wb) / alg[k], 3)
     return res
+
+
+def mfma_child(ie):
+    """Workload of the MFMA-utilisation pass: the headline GEMM, 50 launches
+    to bring the clock up, then 20 measured ones."""
+    import torch
+
+    inp = headline_inputs(ie)
+    bench_headline(ie, inp, 20, 50)
+    torch.cuda.synchronize()
+
+
+def measure_mfma_util(n_last=20, simds=1024, xcds=8):
+    """MfmaUtil of the headline kernel as rocprofv3 defines it
+    (counter_defs.yaml: SQ_VALU_MFMA_BUSY_CYCLES summed / (GRBM_GUI_ACTIVE per
+    XCD x SIMD_NUM)), the clock it implies, over the last n_last launches.
+    GRBM_GUI_ACTIVE is reported summed over the XCDs, so it is divided by
+    their count; the duration comes from the same run's kernel trace."""
+    got = _pmc_rows(["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"], "--mfma-child", extra=["--kernel-trace"])
+    if got is None:
+        return None
+    rows, trace = got
+    busy, grbm = {}, {}
+    for row in rows:
+        if "gemm_i8_256_kernel" not in row["Kernel_Name"]:
+            continue
+        did = row.get("Dispatch_Id", str(len(busy)))
+        tgt = busy if row["Counter_Name"] == "SQ_VALU_MFMA_BUSY_CYCLES" else grbm
+        tgt[did] = tgt.get(did, 0.0) + float(row["Counter_Value"])
+    ids = sorted(set(busy) & set(grbm), key=int)[-n_last:]
+    if not ids:
+        return None
+    dur = {}
+    for t in trace:
+        if "gemm_i8_256_kernel" in t.get("Kernel_Name", "") and t.get("Dispatch_Id") in ids:
+            dur[t["Dispatch_Id"]] = int(t["End_Timestamp"]) - int(t["Start_Timestamp"])
+    b = sum(busy[i] for i in ids) / len(ids)
+    gx = sum(grbm[i] for i in ids) / len(ids) / xcds
+    r = {"mfma_util": round(b / (gx * simds), 4), "sq_valu_mfma_busy_cycles": int(b),
+         "grbm_gui_active_per_xcd": int(gx), "launches": len(ids)}
+    if dur:
+        ns = sum(dur.values()) / len(dur)
+        r["kernel_us"] = round(ns / 1e3, 2)
+        r["clock_mhz"] = round(gx / ns * 1e3, 1)
+        r["tops_at_this_clock_peak"] = round(5000.0 * (gx / ns * 1e3) / 2400.0, 1)
+    return r
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -509,19 +650,31 @@ def cpu_baseline(inputs, budget_s=12.0):
                       f"+ dequant, OpenMP over rows, {dt:.1f} s"}
 
 
-def cpu_baseline_attn(B=32, ctx=8192, seed=8192, budget_s=8.0):
-    """The oracle's decode attention (the reference's split-K algorithm in fp64,
-    tests/test_paged_attention.cu:138-179 as the BASELINE plan restates it),
-    OpenMP over (sequence, query head), on the cfg4 ctx 8192 fp32 workload
-    (same shapes and length law; U(-1,1) data), repeated until budget_s of
-    timed work."""
+def _cpu_threads():
+    return min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+
+
+def _cpu_model():
+    import platform
+    import subprocess
+
+    try:
+        for ln in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if ln.startswith("Model name:"):
+                return ln.split(":", 1)[1].strip()
+    except Exception:  # noqa: BLE001 - informational only
+        pass
+    return platform.processor() or "unknown"
+
+
+def _attn_workload(B, H_q, H_kv, d, ctx, uniform, seed):
+    """Host paged cache for the CPU baselines: U(-1,1) data, shuffled block
+    table, lengths ctx (uniform) or U[ctx/2, ctx]."""
     import numpy as np
 
-    from oracle import orc
-
-    H_q, H_kv, d, bs = 32, 8, 128, 16
+    bs = 16
     r = np.random.default_rng(seed)
-    lens = r.integers(ctx // 2, ctx + 1, B).astype(np.int32)
+    lens = np.full(B, ctx, np.int32) if uniform else r.integers(ctx // 2, ctx + 1, B).astype(np.int32)
     nbs = (lens + bs - 1) // bs
     P, nbps = int(nbs.sum()), int(nbs.max())
     kc = r.random((P, bs, H_kv, d), dtype=np.float32) * 2 - 1
@@ -533,7 +686,25 @@ def cpu_baseline_attn(B=32, ctx=8192, seed=8192, budget_s=8.0):
         table[b, : nbs[b]] = perm[off: off + nbs[b]]
         off += int(nbs[b])
     Q = r.random((B, H_q, d), dtype=np.float32) * 2 - 1
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    return Q, kc, vc, table, lens
+
+
+def _attn_bytes(lens, H_q, H_kv, d, esz=4):
+    nb = int(((lens + 15) // 16).sum())
+    return int(lens.sum()) * H_kv * d * 2 * esz + 2 * len(lens) * H_q * d * 4 + 4 * nb + 4 * len(lens)
+
+
+def cpu_baseline_attn(B=32, ctx=8192, seed=8192, budget_s=8.0):
+    """The oracle's decode attention (the reference's split-K algorithm in fp64,
+    tests/test_paged_attention.cu:138-179 as the BASELINE plan restates it),
+    OpenMP over (sequence, query head), on the cfg4 ctx 8192 fp32 workload
+    (same shapes and length law; U(-1,1) data), repeated until budget_s of
+    timed work."""
+    from oracle import orc
+
+    H_q, H_kv, d, bs = 32, 8, 128, 16
+    Q, kc, vc, table, lens = _attn_workload(B, H_q, H_kv, d, ctx, False, seed)
+    threads = _cpu_threads()
     orc.set_threads(threads)
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -542,19 +713,87 @@ def cpu_baseline_attn(B=32, ctx=8192, seed=8192, budget_s=8.0):
         dt = time.perf_counter() - t0
         if dt >= budget_s:
             break
-    alg = int(lens.sum()) * H_kv * d * 2 * 4 + 2 * B * H_q * d * 4 + 4 * P + 4 * B
+    alg = _attn_bytes(lens, H_q, H_kv, d)
     return {"value": round(alg * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"decode attention cfg4 ctx {ctx} fp32, {B} sequences (Σctx {int(lens.sum())}), the "
                       f"oracle's fp64 split-K restatement, OpenMP over (sequence, head), {reps} calls in {dt:.1f} s"}
 
 
+def _cpu_time(fn, budget_s=1.5, min_runs=5):
+    """Median of >= min_runs calls after one warm-up, or of as many as budget_s
+    allows (at least one)."""
+    fn()
+    ts, start = [], time.perf_counter()
+    while len(ts) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+        if time.perf_counter() - start > budget_s:
+            break
+    ts.sort()
+    return ts[len(ts) // 2], len(ts)
+
+
+def cpu_baseline_detail():
+    """BASELINE's CPU plan: the oracle (C, -O3 x86-64-v3, OpenMP) on cfg1
+    512^3, the GPT-2 weight shapes at M = 1, 4, 16, cfg3 and cfg4 at ctx
+    4096 / 8192, each at 1 thread and at all threads; median of >= 5 runs
+    after a warm-up (fewer, stated, where one run is long)."""
+    import numpy as np
+
+    from oracle import orc
+
+    T = _cpu_threads()
+    out = {"cpu_model": _cpu_model(), "nproc": os.cpu_count(), "threads_all": T, "kind": "port",
+           "gemm": [], "decode_attn": []}
+    r = np.random.default_rng(512)
+    A = r.standard_normal((512, 512)).astype(np.float32)
+    BT = r.standard_normal((512, 512)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Bp, sB = orc.quantize(BT)
+    for th in (1, T):
+        orc.set_threads(th)
+        t, n = _cpu_time(lambda: orc.gemm(Ap, Bp, sA, sB, 0))
+        out["gemm"].append({"workload": "cfg1 M=N=K=512", "threads": th, "ms": round(t * 1e3, 3),
+                            "TOPs": round(2 * 512 ** 3 / t / 1e12, 5), "runs": n})
+    for K, N in [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 50257)]:
+        W = r.integers(-127, 128, (N, K), dtype=np.int8).view(np.int32)
+        sW = (r.random(N, dtype=np.float32) * 0.01).astype(np.float32)
+        for M in (1, 4, 16):
+            X = r.integers(-127, 128, (M, K), dtype=np.int8).view(np.int32)
+            sX = np.ones(M, np.float32)
+            for th in (1, T):
+                orc.set_threads(th)
+                t, n = _cpu_time(lambda: orc.gemm(X, W, sX, sW, 0), budget_s=1.0)
+                out["gemm"].append({"workload": f"GPT-2 M={M} K={K} N={N}", "threads": th,
+                                    "us": round(t * 1e6, 1), "GBps": round(gemm_bytes(M, N, K) / t / 1e9, 3),
+                                    "runs": n})
+    orc.set_threads(T)
+    for name, (B, H_q, H_kv, d, ctx, uni) in (("cfg3 MHA ctx 1024", (8, 12, 12, 64, 1024, True)),
+                                              ("cfg4 GQA ctx 4096", (32, 32, 8, 128, 4096, False)),
+                                              ("cfg4 GQA ctx 8192", (32, 32, 8, 128, 8192, False))):
+        Q, kc, vc, table, lens = _attn_workload(B, H_q, H_kv, d, ctx, uni, ctx + B)
+        for th in (1, T):
+            orc.set_threads(th)
+            # one thread: the first two sequences of cfg4 (a bounded sample)
+            nb = B if (th == T or B <= 8) else 2
+            q, tb, ln = Q[:nb], table[:nb], lens[:nb]
+            t, n = _cpu_time(lambda: orc.decode_attn(q, kc, vc, tb, ln, int(ln.max()), 16, H_kv), budget_s=3.0)
+            out["decode_attn"].append({"workload": name, "threads": th, "sequences": nb, "ms": round(t * 1e3, 2),
+                                       "GBps": round(_attn_bytes(ln, H_q, H_kv, d) / t / 1e9, 3), "runs": n})
+        del Q, kc, vc
+    log(f"cpu detail {out}")
+    return out
+
+
 def main():
     args = parse()
-    if args.pmc_child:
+    if args.pmc_child or args.mfma_child:
         import ie_amd as ie
 
         ie.load()
-        pmc_child(ie)
+        ie.check("ie_init")
+        (pmc_child if args.pmc_child else mfma_child)(ie)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -568,8 +807,24 @@ def main():
     ie.load()
     ie.check("ie_init")
     torch.cuda.synchronize()
+    log("headline operands: 8192^3 INT8 GEMM, quantized untimed")
+    inputs = headline_inputs(ie)
+    legs = {}
+    if not args.only_headline:
+        if "gemv" not in skip:
+            legs["gemv"] = bench_gemv(ie)
+        if "gemm512" not in skip:
+            legs["gemm_m512"] = bench_gemm512(ie)
+        if "ref" not in skip:
+            legs["ref_shapes"] = bench_ref_shapes(ie)
+        if "attn" not in skip:
+            legs["decode_attn"] = bench_attn(ie)
+        if "e2e" not in skip:
+            legs["e2e_gpt2"] = bench_e2e(ie)
+        if "sampler" not in skip:
+            legs["sampler"] = bench_sampler(ie)
     log("headline: 8192^3 INT8 GEMM")
-    h = bench_headline(ie, args.steps, args.warmup)
+    h = bench_headline(ie, inputs, args.steps, args.warmup)
     res = {
         "metric": METRIC,
         "value": round(h["value"], 2),
@@ -586,42 +841,51 @@ def main():
         "config": {"workload": "INT8 GEMM M=N=K=8192, NT layout, Plain epilogue (BASELINE configs[1])",
                    "M": 8192, "N": 8192, "K": 8192, "parallelism": "none (1 GPU)"},
         "roofline": roof(h["kernel_tops"], PEAK_I8_TOPS, "TOP/s", "mfma"),
+        "headline_order": ("operands made first; warm-up and timed launches after the other GPU legs"
+                           if legs else "warm-up and timed launches right after the operands are made"),
     }
     if "vendor" not in skip:
-        res["vendor_gemm"] = bench_vendor(ie, h["inputs"], args.steps, args.warmup)
+        res["vendor_gemm"] = bench_vendor(ie, inputs, args.steps, args.warmup)
         log(f"vendor {res['vendor_gemm']}")
-    if not args.only_headline:
-        if "gemv" not in skip:
-            res["gemv"] = bench_gemv(ie)
-            dom = [r for r in res["gemv"] if (r["M"], r["K"], r["N"]) == (1, 8192, 28672)][0]
-            res["gemv_roofline"] = roof(dom["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
-            res["gemv_roofline"]["kernel"] = "gemv M=1 K=8192 N=28672 (decode GEMV, 235 MB of weights)"
-        if "gemm512" not in skip:
-            res["gemm_m512"] = bench_gemm512(ie)
-        if "attn" not in skip:
-            res["decode_attn"] = bench_attn(ie)
-            c8 = [r for r in res["decode_attn"] if r["ctx"] == 8192 and r["kv"] == "fp32"][0]
-            res["decode_attn_roofline"] = roof(c8["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
-            res["decode_attn_roofline"]["kernel"] = "decode_attn cfg4 ctx 8192 fp32"
-        if "e2e" not in skip:
-            res["e2e_gpt2"] = bench_e2e(ie)
-        if "sampler" not in skip:
-            res["sampler"] = bench_sampler(ie)
+    res.update(legs)
+    if "gemv" in legs:
+        rows = {(r["M"], r["K"], r["N"]): r for r in legs["gemv"]}
+        dom = rows[(1, 8192, 8192)]
+        res["gemv_roofline"] = roof(dom["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
+        res["gemv_roofline"]["kernel"] = "decode GEMV M=1 K=N=8192 (BASELINE configs[1], 67 MB of weights)"
+        res["gemv_roofline"]["rows"] = [
+            {"shape": f"M={M} K={K} N={N}", "frac": rows[(M, K, N)]["frac_hbm"],
+             "baseline_shape": N != 28672}
+            for M, K, N in [(1, 8192, 8192), (4, 8192, 8192), (16, 8192, 8192), (1, 768, 50257), (4, 768, 50257),
+                            (16, 768, 50257), (1, 8192, 28672), (4, 8192, 28672), (16, 8192, 28672)]]
+    if "decode_attn" in legs:
+        c8 = [r for r in legs["decode_attn"] if r["ctx"] == 8192 and r["kv"] == "fp32" and r["H_q"] == 32][0]
+        res["decode_attn_roofline"] = roof(c8["GBps"], PEAK_HBM_GBS, "GB/s", "hbm")
+        res["decode_attn_roofline"]["kernel"] = "decode_attn cfg4 ctx 8192 fp32"
     if "cpu" not in skip:
         log("cpu baseline")
-        res["cpu_baseline"] = cpu_baseline(h["inputs"])
+        res["cpu_baseline"] = cpu_baseline(inputs)
+        res["cpu_baseline"]["cpu_model"] = _cpu_model()
         res["cpu_baseline_attn"] = cpu_baseline_attn()
         log(f"cpu attention {res['cpu_baseline_attn']}")
+        res["cpu_baseline_detail"] = cpu_baseline_detail()
     if not args.no_traffic:
+        if "mfma" not in skip:
+            log("MFMA utilisation (rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / GRBM_GUI_ACTIVE pass)")
+            res["roofline"]["mfma"] = measure_mfma_util()
+            log(f"mfma {res['roofline']['mfma']}")
         log("traffic (rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
         t = measure_traffic()
         res["traffic_detail"] = t
-        if t and "gemm" in t:
-            res["roofline"]["traffic"] = t["gemm"]["fetch_bytes"] + t["gemm"]["write_bytes"]
-        if t and "gemv" in t and "gemv_roofline" in res:
-            res["gemv_roofline"]["traffic"] = t["gemv"]["fetch_bytes"] + t["gemv"]["write_bytes"]
-        if t and "attn" in t and "decode_attn_roofline" in res:
-            res["decode_attn_roofline"]["traffic"] = t["attn"]["fetch_bytes"] + t["attn"]["write_bytes"]
+
+        def traffic(k):
+            return t[k]["fetch_bytes"] + t[k]["write_bytes"] if t and k in t else None
+
+        res["roofline"]["traffic"] = traffic("gemm")
+        if "gemv_roofline" in res:
+            res["gemv_roofline"]["traffic"] = traffic("gemv_8192_m1")
+        if "decode_attn_roofline" in res:
+            res["decode_attn_roofline"]["traffic"] = traffic("attn")
     print(json.dumps(res), flush=True)
 
 

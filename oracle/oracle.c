@@ -193,26 +193,30 @@ int orc_int8_gemm(int M, int N, int K, const int32_t* A_packed,
     if (epi == 3 && !residual) return 1;
     const int K4 = K / 4;
     int8_t* bt = (int8_t*)malloc((size_t)N * (K ? K : 1));
-    if (!bt) return 2;
+    int8_t* at = (int8_t*)malloc((size_t)M * (K ? K : 1));
+    if (!bt || !at) {
+        free(bt);
+        free(at);
+        return 2;
+    }
 #pragma omp parallel for schedule(static)
     for (int j = 0; j < N; ++j) unpack_row(BT_packed + (size_t)j * K4, K, bt + (size_t)j * K);
-#pragma omp parallel
-    {
-        int8_t* a = (int8_t*)malloc((size_t)(K ? K : 1));
-#pragma omp for schedule(static)
-        for (int i = 0; i < M; ++i) {
-            unpack_row(A_packed + (size_t)i * K4, K, a);
-            for (int j = 0; j < N; ++j) {
-                const int8_t* b = bt + (size_t)j * K;
-                int32_t s = 0;
-                for (int k = 0; k < K; ++k) s += (int32_t)a[k] * (int32_t)b[k];
-                float bv = bias ? bias[j] : 0.0f;
-                float rv = residual ? residual[(size_t)i * N + j] : 0.0f;
-                C[(size_t)i * N + j] = epilogue(epi, s, scale_A[i], scale_B[j], bv, rv);
-            }
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; ++i) unpack_row(A_packed + (size_t)i * K4, K, at + (size_t)i * K);
+    /* every (row, column) output on its own: the threads share decode-sized M too */
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int i = 0; i < M; ++i) {
+        for (int j = 0; j < N; ++j) {
+            const int8_t* a = at + (size_t)i * K;
+            const int8_t* b = bt + (size_t)j * K;
+            int32_t s = 0;
+            for (int k = 0; k < K; ++k) s += (int32_t)a[k] * (int32_t)b[k];
+            float bv = bias ? bias[j] : 0.0f;
+            float rv = residual ? residual[(size_t)i * N + j] : 0.0f;
+            C[(size_t)i * N + j] = epilogue(epi, s, scale_A[i], scale_B[j], bv, rv);
         }
-        free(a);
     }
+    free(at);
     free(bt);
     return 0;
 }
