@@ -69,6 +69,8 @@ def parse():
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE passes")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--mfma-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--ramp", action="store_true",
+                    help="per-launch times of the headline GEMM in bursts (power transient), then exit")
     return ap.parse_args()
 
 
@@ -367,7 +369,7 @@ def bench_e2e(ie):
 
     out = []
     rng = np.random.default_rng(128)
-    # fused step (5 launches per layer) for both LM heads; the unfused step
+    # fused step (4 launches per layer up to 384 tokens) for both LM heads; the unfused step
     # (every operation through the public C ABI) and the fp32 vendor-GEMM
     # backend (the reference's CUBLAS_FP32 comparison point) for comparison
     for head_i8, fuse, backend in ((False, True, 0), (True, True, 0), (False, False, 0), (False, False, 1)):
@@ -571,6 +573,37 @@ def measure_traffic():
                 res[k]["algorithmic_bytes"] = alg[k]
                 res[k]["traffic_over_algorithmic"] = round((fb + wb) / alg[k], 3)
     return res
+
+
+def ramp_bursts(ie):
+    """Per-launch µs of the headline GEMM (HIP events around each launch):
+    60 back-to-back launches on fresh operands, 30 more after 300 ms idle, 30
+    into a fresh output buffer, and 30 on all-zero operands (little bit
+    toggling, so little power)."""
+    import torch
+
+    Ap, Bp, sA, sB = headline_inputs(ie)
+    C = torch.empty((8192, 8192), device="cuda")
+
+    def burst(n):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for a, b in ev:
+            a.record()
+            ie.int8_gemm(Ap, Bp, sA, sB, ie.EPI_PLAIN, out=C)
+            b.record()
+        torch.cuda.synchronize()
+        return [round(a.elapsed_time(b) * 1e3, 1) for a, b in ev]
+
+    out = {"burst1": burst(60)}
+    time.sleep(0.3)
+    out["after_300ms_idle"] = burst(30)
+    C = torch.empty((8192, 8192), device="cuda")
+    out["fresh_output"] = burst(30)
+    Ap.zero_()
+    Bp.zero_()
+    torch.cuda.synchronize()
+    out["zero_operands"] = burst(30)
+    print(json.dumps(out), flush=True)
 
 
 def mfma_child(ie):
@@ -788,12 +821,12 @@ def cpu_baseline_detail():
 
 def main():
     args = parse()
-    if args.pmc_child or args.mfma_child:
+    if args.pmc_child or args.mfma_child or args.ramp:
         import ie_amd as ie
 
         ie.load()
         ie.check("ie_init")
-        (pmc_child if args.pmc_child else mfma_child)(ie)
+        (pmc_child if args.pmc_child else mfma_child if args.mfma_child else ramp_bursts)(ie)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "

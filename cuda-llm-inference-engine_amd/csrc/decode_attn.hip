@@ -42,6 +42,7 @@
 #include <map>
 #include <mutex>
 
+#include "attn_split.h"
 #include "device_util.h"
 #include "ie_internal.h"
 
@@ -65,140 +66,6 @@ template <int D, typename KV, int G>
 constexpr int wave_heads() { return (D == 128 && sizeof(KV) == 4) || (D == 128 && G == 8) ? 4 : 8; }
 template <int D, typename KV, int G>
 constexpr int wave_ring() { return D == 128 && sizeof(KV) == 4 && G < 8 ? 4 : 2; }
-
-// Raw K/V words of one lane's d/16-element slice of one token; bf16 stays
-// packed until use so a prefetched chunk costs half the registers.
-template <int EPL, typename KV>
-struct Slice {
-    static constexpr int WORDS = EPL * (int)sizeof(KV) / 4;
-    uint32_t w[WORDS];
-};
-
-template <int EPL, typename KV>
-__device__ __forceinline__ void load_raw(const KV* __restrict__ p, Slice<EPL, KV>& s) {
-    constexpr int W = Slice<EPL, KV>::WORDS;
-    if constexpr (W % 4 == 0) {
-#pragma unroll
-        for (int i = 0; i < W / 4; ++i) {
-            const uint4 v = reinterpret_cast<const uint4*>(p)[i];
-            s.w[4 * i + 0] = v.x;
-            s.w[4 * i + 1] = v.y;
-            s.w[4 * i + 2] = v.z;
-            s.w[4 * i + 3] = v.w;
-        }
-    } else {
-        static_assert(W == 2, "slice width");
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        s.w[0] = v.x;
-        s.w[1] = v.y;
-    }
-}
-
-template <int EPL, typename KV>
-__device__ __forceinline__ float elem(const Slice<EPL, KV>& s, int e) {
-    if constexpr (sizeof(KV) == 4) {
-        return __builtin_bit_cast(float, s.w[e]);
-    } else {
-        const uint32_t w = s.w[e >> 1];
-        return __builtin_bit_cast(float, (e & 1) ? (w & 0xffff0000u) : (w << 16));
-    }
-}
-
-template <int EPL>
-__device__ __forceinline__ void load_q(const float* __restrict__ p, float (&out)[EPL]) {
-#pragma unroll
-    for (int i = 0; i < EPL / 4; ++i) {
-        const float4 v = reinterpret_cast<const float4*>(p)[i];
-        out[4 * i + 0] = v.x;
-        out[4 * i + 1] = v.y;
-        out[4 * i + 2] = v.z;
-        out[4 * i + 3] = v.w;
-    }
-}
-
-// A chunk of 4T tokens: lane row grp holds tokens c0 + 4j + grp, j < T.
-template <int D, typename KV, int T>
-struct Chunk {
-    static constexpr int EPL = D / 16;
-    Slice<EPL, KV> k[T], v[T];
-    bool valid[T];
-};
-
-// Loads this lane's slices of tokens c0 + 4j + grp (j < T) of a chunk.
-template <int D, typename KV, int T>
-__device__ __forceinline__ void load_chunk(Chunk<D, KV, T>& c, int c0, int grp, int tok1,
-                                           const int* __restrict__ bt, int block_size,
-                                           size_t tok_stride, const KV* kbase, const KV* vbase) {
-// Branch-free: positions past tok1 re-read token tok1-1 (a cache hit) and are
-// masked by `valid`, so the loads never sit in divergent control flow and the
-// compiler can keep the next chunk in flight across the current one.
-#pragma unroll
-    for (int j = 0; j < T; ++j) {
-        const int pos = c0 + 4 * j + grp;
-        c.valid[j] = pos < tok1;
-        const int pc = min(pos, tok1 - 1);
-        const int blk = pc / block_size;
-        const size_t row = (size_t)bt[blk] * block_size + (pc - blk * block_size);
-        load_raw(kbase + row * tok_stride, c.k[j]);
-        load_raw(vbase + row * tok_stride, c.v[j]);
-    }
-}
-
-// Block size 16: the chunk's tokens (c0 a multiple of 4T) lie in blocks
-// phys[0], phys[1], ... (16 tokens each), the same for every lane.
-template <int D, typename KV, int T>
-__device__ __forceinline__ void load_chunk16(Chunk<D, KV, T>& c, int c0, int grp, int tok1,
-                                             const int (&phys)[(T + 3) / 4], size_t tok_stride,
-                                             const KV* kbase, const KV* vbase) {
-#pragma unroll
-    for (int j = 0; j < T; ++j) {
-        const int pos = c0 + 4 * j + grp;
-        c.valid[j] = pos < tok1;
-        const int pc = min(pos, tok1 - 1);
-        const size_t row = (size_t)phys[j / 4] * 16 + (pc & 15);
-        load_raw(kbase + row * tok_stride, c.k[j]);
-        load_raw(vbase + row * tok_stride, c.v[j]);
-    }
-}
-
-template <int D, int G, typename KV, int T>
-__device__ __forceinline__ void consume_chunk(const Chunk<D, KV, T>& c, const float (&q)[G][D / 16],
-                                              float (&m)[G], float (&l)[G], float (&o)[G][D / 16]) {
-    constexpr int EPL = D / 16;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float s[T];
-#pragma unroll
-        for (int j = 0; j < T; ++j) {
-            float dot = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) dot = fmaf(q[g][e], elem(c.k[j], e), dot);
-            dot = row16_sum(dot);
-            s[j] = c.valid[j] ? dot : -INFINITY;
-        }
-        float cm = s[0];
-#pragma unroll
-        for (int j = 1; j < T; ++j) cm = fmaxf(cm, s[j]);
-        cm = max_xor32(max_xor16(cm));
-        const float mn = fmaxf(m[g], cm);
-        const float alpha = exp2f(m[g] - mn);
-        float p[T], psum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < T; ++j) {
-            p[j] = exp2f(s[j] - mn);
-            psum += p[j];
-        }
-        l[g] = fmaf(l[g], alpha, psum);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float acc = o[g][e] * alpha;
-#pragma unroll
-            for (int j = 0; j < T; ++j) acc = fmaf(p[j], elem(c.v[j], e), acc);
-            o[g][e] = acc;
-        }
-        m[g] = mn;
-    }
-}
 
 // Merges the S split partials (o[D], m, l) of one (b, query head) with one
 // wave: lanes read the (m, l) of 64 splits at a time in parallel, and the
@@ -440,110 +307,6 @@ done:
     }
 }
 
-// WPS waves per split: 4 for short splits (the waves take the split's chunks
-// round-robin and merge in LDS), 1 for long ones (no LDS merge, no barrier).
-// BS16: block_size == 16 (the engine's and the reference's), see below.
-// Partial softmax state (m, l, o) over tokens [tok0, tok1) of sequence b for
-// the G query heads of KV head kvh; the split's WPS waves take its 16-token
-// chunks round-robin (this one is `wave`).  bt is the sequence's block-table
-// row.  On return every lane holds the wave's totals (o summed over the four
-// lane rows).
-template <int D, int G, typename KV, int WPS, bool BS16, int R>
-__device__ __forceinline__ void split_partial(const float* __restrict__ Q, const KV* __restrict__ kcache,
-                                              const KV* __restrict__ vcache, const int* __restrict__ bt,
-                                              int b, int kvh, int H_q, int H_kv, int block_size, int tok0,
-                                              int tok1, int wave, int lane, float qscale, float (&m)[G],
-                                              float (&l)[G], float (&o)[G][D / 16]) {
-    constexpr int EPL = D / 16;
-    // Chunk rows and ring depth: R chunks of 4T tokens cycle through the
-    // registers, R - 1 of them in flight while one is computed.  fp32 with
-    // d = 128 takes 8-token chunks so four fit where two 16-token ones did.
-    constexpr int T = 4;              // lane rows hold T tokens each
-    constexpr int CT = 4 * T;         // tokens per chunk
-    constexpr int STEP = CT * WPS;    // tokens per round of the split's waves
-    const int grp = lane >> 4, li = lane & 15;
-    const size_t tok_stride = (size_t)H_kv * D;
-    // d = 128 bf16 rings keep their loads in place (measured 2-5% faster at
-    // ctx 4096-32768); fp32 rings need the register room sinking gives them
-    // and d = 64 bf16 measured 9% slower.
-    constexpr bool OPQ = sizeof(KV) == 2 && D == 128;
-    const KV* kbase = (OPQ ? opaque_global(kcache) : kcache) + (size_t)kvh * D + li * EPL;
-    const KV* vbase = (OPQ ? opaque_global(vcache) : vcache) + (size_t)kvh * D + li * EPL;
-
-    // Each wave walks its chunks, keeping the next R - 1 chunks' loads in
-    // flight while it computes the current one.  With block size 16 a chunk
-    // lies in one block, so its physical block id is wave-uniform: it comes
-    // from a scalar load issued one chunk ahead (pn), which does not wait
-    // behind the in-flight KV loads as a vector load would (they retire in
-    // issue order), so the next KV loads go out as soon as a chunk is done.
-    // Chunks past the end re-read the last token (masked), so every step
-    // issues the same loads and the ring needs no branches.
-    Chunk<D, KV, T> buf[R];
-    int c0 = tok0 + wave * CT;
-    constexpr int NPH = (T + 3) / 4;  // blocks per chunk
-    auto phys = [&](int cs) { return bt[min(cs, tok1 - 1) >> 4]; };
-    int pn[NPH];
-    auto prefetch = [&](int cs) {
-#pragma unroll
-        for (int k = 0; k < NPH; ++k) pn[k] = phys(cs + 16 * k);
-    };
-    if constexpr (BS16) prefetch(c0);
-    auto next = [&](Chunk<D, KV, T>& c, int cs) {
-        if constexpr (BS16) {
-            load_chunk16(c, cs, grp, tok1, pn, tok_stride, kbase, vbase);
-            prefetch(cs + STEP);
-        } else {
-            load_chunk(c, cs, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
-        }
-    };
-    const bool any = c0 < tok1;
-    if (any) {
-#pragma unroll
-        for (int p = 0; p < R - 1; ++p) next(buf[p], c0 + p * STEP);
-    }
-
-    float q[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        load_q<EPL>(Q + ((size_t)b * H_q + (size_t)kvh * G + g) * D + li * EPL, q[g]);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) q[g][e] *= qscale;
-    }
-
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
-    }
-
-    // Each step issues the chunk R - 1 rounds ahead into the buffer consumed
-    // last, then consumes the current one.
-    if (any) {
-        while (true) {
-#pragma unroll
-            for (int u = 0; u < R; ++u) {
-                next(buf[(u + R - 1) % R], c0 + (R - 1) * STEP);
-                consume_chunk<D, G, KV, T>(buf[u], q, m, l, o);
-                c0 += STEP;
-                if (c0 >= tok1) goto done;
-            }
-        }
-    }
-done:
-
-    // The four lane rows share the wave's running max: plain sums merge them.
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        l[g] = sum_xor32(sum_xor16(l[g]));
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            o[g][e] = sum_xor32(sum_xor16(o[g][e]));
-        }
-    }
-}
-
 // With WPS == 1 a workgroup holds blockDim.x / 64 waves, one per KV head
 // (kv head = blockIdx.y * waves + wave), all on the same split.
 template <int D, int G, typename KV, int WPS, bool BS16, int R, int NT>
@@ -599,48 +362,7 @@ __global__ __launch_bounds__(NT) void decode_attn_split_kernel(
         }
         return;
     } else {
-        __shared__ float sm_m[WPS][G], sm_l[WPS][G];
-        __shared__ float sm_o[WPS][G][D];
-        if (grp == 0) {
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) sm_o[wave][g][li * EPL + e] = o[g][e];
-        }
-        if (lane == 0) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                sm_m[wave][g] = m[g];
-                sm_l[wave][g] = l[g];
-            }
-        }
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < G * D; idx += 64 * WPS) {
-            const int g = idx / D, dd = idx - (idx / D) * D;
-            float mx = sm_m[0][g];
-#pragma unroll
-            for (int w = 1; w < WPS; ++w) mx = fmaxf(mx, sm_m[w][g]);
-            float ov = 0.0f, lv = 0.0f;
-            if (mx != -INFINITY) {
-#pragma unroll
-                for (int w = 0; w < WPS; ++w) {
-                    const float f = exp2f(sm_m[w][g] - mx);
-                    ov = fmaf(sm_o[w][g][dd], f, ov);
-                    lv = fmaf(sm_l[w][g], f, lv);
-                }
-            }
-            const size_t bh = (size_t)b * H_q + (size_t)kvh * G + g;
-            if (num_splits == 1) {
-                O[bh * D + dd] = ov * (lv > 0.0f ? 1.0f / lv : 0.0f);
-                continue;
-            }
-            float* dst = ws + (bh * num_splits + split) * (D + 2);
-            dst[dd] = ov;
-            if (dd == 0) {
-                dst[D] = mx;
-                dst[D + 1] = lv;
-            }
-        }
+        split_finish_lds<D, G, WPS>(b, kvh, H_q, split, num_splits, wave, lane, m, l, o, ws, O);
     }
 }
 

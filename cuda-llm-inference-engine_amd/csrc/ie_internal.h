@@ -61,6 +61,14 @@ struct GemvFusion {
     int block_size = 16;
     int* ctx_lens = nullptr;
 };
+// The engine's QKV projection + decode attention in one launch, one
+// workgroup per (sequence, head) (qkv_attn.hip): f as for the kEpiQKV GEMV
+// with src kSrcLnQuant (x, LayerNorm gamma/beta), a one-split plan; O [B, d]
+// receives the attention output.  Bit-identical to launch_gemv_fused(QKV)
+// followed by launch_decode_attn with one split.
+bool qkv_attn_supported(int d_model, int n_heads, int d_head, int block_size);
+void launch_qkv_attn(int B, int H, const int32_t* BT, const float* sB, const float* bias, const GemvFusion& f,
+                     float* O, hipStream_t s);
 // Whether launch_gemv_fused has a kernel for this combination (M <= 16).
 bool gemv_fused_supported(int M, int K, int src, int epi);
 void launch_gemv_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s);
@@ -169,6 +177,16 @@ void launch_embedding_batch(int B, const int* ids, const int* positions, int d,
                             hipStream_t s);
 void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits,
                        int d, int V, hipStream_t s);
+// The decode step's head in one launch (support.hip): final LayerNorm of the
+// rows x [rows, d] (the standalone LayerNorm's bits), fp32 LM head over wte
+// into logits [rows, V], and each row's first-maximum index merged into
+// keys[row] (cleared to 0 beforehand); launch_head_finalize then writes the
+// token ids, clears the keys and (advance) moves the positions on.
+bool vocab_head_supported(int rows, int d);
+void launch_vocab_head(int rows, const float* x, const float* gamma, const float* beta, float eps,
+                       const float* wte, float* logits, int d, int V, unsigned long long* keys, hipStream_t s);
+void launch_head_finalize(int B, unsigned long long* keys, int* tokens, int* positions, bool advance,
+                          hipStream_t s);
 void launch_argmax(int rows, const float* logits, int n, int* out,
                    hipStream_t s);
 

@@ -1,0 +1,117 @@
+// qkv_attn.hip — the engine's QKV projection and decode attention in one
+// launch, one workgroup per (sequence b, head h).
+//
+// In a decode step the attention of head h of sequence b needs only that
+// head's q, k and v (and the cache), not the other heads' outputs, so the
+// QKV projection and the attention need no grid-wide step between them when
+// a workgroup owns the head's 3 x D projection rows.  The workgroup
+//   1. requests the head's 3 x D weight rows and their epilogue operands,
+//   2. builds the int8 activation row of x[b] in LDS (LayerNorm + per-row
+//      quantizer: stage_row, as the fused GEMV prologue),
+//   3. computes the rows with dot4 and the 16-lane DPP reduction and stores
+//      them as the QKV epilogue does: q to Q, k and v appended to the cache at
+//      the sequence's position (src/gpt2_engine.cu:464-481 of the reference),
+//   4. walks the head's cached tokens with split_partial on its 8 waves and
+//      merges them in LDS (split_finish_lds), as decode_attn_split_kernel does
+//      for a one-split plan (src/gpt2_engine.cu:496-504 / K13).
+// Every value is produced by the same device code in the same order as the
+// QKV GEMV + attention kernel pair, so the outputs are bit-identical to that
+// pair (and to the step built from the C ABI).  One launch per layer fewer:
+// GPT-2 Small, d = 768, D = 64, block size 16, a one-split plan.
+#include "attn_split.h"
+#include "gemv_common.h"
+#include "ie_internal.h"
+
+namespace ie {
+namespace {
+
+constexpr int kQaWaves = 8;  // the 8-wave form of the one-split attention
+constexpr int kQaK = 768;    // d_model (the projection's K)
+
+template <int D, typename KV>
+__global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* __restrict__ BT,
+                                                                 const float* __restrict__ sB,
+                                                                 const float* __restrict__ bias, GemvFusion f,
+                                                                 const KV* __restrict__ kcache,
+                                                                 const KV* __restrict__ vcache, int H,
+                                                                 float qscale, float* __restrict__ O) {
+    constexpr int K16 = kQaK / 16, CPL = K16 / 16;  // 16-byte chunks per row, per lane
+    constexpr int RPW = 3 * D / kQaWaves;           // projection rows per wave
+    constexpr int G = RPW / 4;                      // 4-row groups per wave
+    static_assert(RPW % 4 == 0 && K16 % 16 == 0, "head rows split into 4-row groups");
+    constexpr int d = kQaK;
+    __shared__ i32x4 a_lds[K16];
+    __shared__ float s_sa[1];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int lane = threadIdx.x & 63, li = lane & 15;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    // Row 0 of this view is sequence b.
+    GemvFusion fb = f;
+    fb.q = f.q + (size_t)b * d;
+    fb.positions = f.positions + b;
+    fb.table = f.table + (size_t)b * f.nbps;
+    fb.ctx_lens = f.ctx_lens + b;
+
+    // Projection row of lane group (wave wv, group g): q, k or v row i of head h.
+    auto row_of = [&](int g) {
+        const int lr = (wv * G + g) * 4 + (lane >> 4);
+        const int which = lr / D;
+        return which * d + h * D + (lr - which * D);
+    };
+    const i32x4* w4 = reinterpret_cast<const i32x4*>(BT);
+    i32x4 wreg[G][CPL];
+    EpiIn ein[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) ein[g] = epi_load<IE_EPI_BIAS>(0, row_of(g), 3 * d, sB, bias, nullptr);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const i32x4* w = w4 + (size_t)row_of(g) * K16 + li;
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) wreg[g][t] = w[16 * t];
+    }
+    size_t slot[1];
+    qkv_slots<1>(fb, 1, slot);
+
+    if (wv == 0) stage_row<kQaK, kSrcLnQuant>(f.x + (size_t)b * d, f, reinterpret_cast<int32_t*>(a_lds), &s_sa[0],
+                                             lane);
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        int32_t acc[1] = {0};
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) dot_chunk<1>(acc, wreg[g][t], a_lds, K16, li + 16 * t);
+        gemv_finish<1, kEpiQKV>(acc, li, row_of(g), true, 1, 3 * d, s_sa, ein[g], slot, nullptr, fb);
+    }
+    // The head's q and its new cache row are read back below.
+    __syncthreads();
+
+    // Tokens 0 .. pos of the sequence (never past its block-table row).
+    const int ctx = f.positions[b] + 1;
+    const int tok1 = (int)min((long long)ctx, (long long)f.nbps * f.block_size);
+    float m[1], l[1], o[1][D / 16];
+    split_partial<D, 1, KV, kQaWaves, true, 2>(f.q, kcache, vcache, fb.table, b, h, H, H, f.block_size, 0, tok1,
+                                                wv, lane, qscale, m, l, o);
+    split_finish_lds<D, 1, kQaWaves>(b, h, H, 0, 1, wv, lane, m, l, o, nullptr, O);
+}
+
+}  // namespace
+
+bool qkv_attn_supported(int d_model, int n_heads, int d_head, int block_size) {
+    return d_model == kQaK && d_head == 64 && n_heads * d_head == d_model && block_size == 16;
+}
+
+void launch_qkv_attn(int B, int H, const int32_t* BT, const float* sB, const float* bias, const GemvFusion& f,
+                     float* O, hipStream_t s) {
+    constexpr int D = 64;
+    const float qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+    const dim3 grid(H, B);
+    if (f.kv_dtype == IE_KV_BF16)
+        qkv_attn_kernel<D, uint16_t><<<grid, 64 * kQaWaves, 0, s>>>(
+            BT, sB, bias, f, static_cast<const uint16_t*>(f.kc), static_cast<const uint16_t*>(f.vc), H, qscale, O);
+    else
+        qkv_attn_kernel<D, float><<<grid, 64 * kQaWaves, 0, s>>>(
+            BT, sB, bias, f, static_cast<const float*>(f.kc), static_cast<const float*>(f.vc), H, qscale, O);
+}
+
+}  // namespace ie

@@ -131,30 +131,90 @@ __global__ __launch_bounds__(256) void vocab_proj_kernel(int rows, const float* 
 // A logit depends on its own hidden row only (zero columns add nothing to
 // the others), so a batch of 16 and a batch of 1 give the same bits per row.
 // Plain loads: non-temporal ones measured ~10% slower here.
-template <int NCH>
+//
+// Key of a (logit, index) pair whose unsigned maximum is the first index of
+// the largest logit: the value in an order-preserving bit pattern (-0 taken
+// as +0, as a float comparison does) above the complement of the index.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// HEAD: the decode step's head in one launch.  h is then the hidden state x
+// before the final LayerNorm: the workgroup first normalises the rows into
+// LDS with the standalone LayerNorm's arithmetic (ln_*, one wave per row, the
+// same lane order, so the same bits), and the argmax of each row (first index
+// of the maximum) is folded in: every workgroup keeps its rows' best (value,
+// index) while it writes the logits and merges it into keys[row] with one
+// 64-bit atomic max (argmax_key); head_finalize_kernel turns the keys into
+// token ids.
+struct HeadArgs {
+    const float* gamma = nullptr;
+    const float* beta = nullptr;
+    float eps = 1e-5f;
+    unsigned long long* keys = nullptr;
+};
+
+template <int NCH, bool HEAD = false>
 __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const float* __restrict__ h,
                                                                  const float* __restrict__ wte,
-                                                                 float* __restrict__ logits, int d, int V) {
+                                                                 float* __restrict__ logits, int d, int V,
+                                                                 HeadArgs ha) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     __shared__ f32x4 red[2][4][64];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i = lane & 15, g = lane >> 4;
     const int kq = w * NCH * 64;
-    float4 hb[NCH][4];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            hb[c][e] = i < rows ? *reinterpret_cast<const float4*>(h + (size_t)i * d + kq + 64 * c + 16 * e + 4 * g)
-                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const int ntiles = (V + 15) / 16;
+    // provenance hidden, so the compiler keeps the first tile's loads where
+    // they are issued instead of sinking them past the LayerNorm to their use
+    const float* wsrc = HEAD ? opaque_global(wte) : wte;
     auto load = [&](float4 (&b)[NCH][4], int t) {
-        const float* p = wte + (size_t)min(min(t, ntiles - 1) * 16 + i, V - 1) * d + kq + 4 * g;
+        const float* p = wsrc + (size_t)min(min(t, ntiles - 1) * 16 + i, V - 1) * d + kq + 4 * g;
 #pragma unroll
         for (int c = 0; c < NCH; ++c)
 #pragma unroll
             for (int e = 0; e < 4; ++e) b[c][e] = *reinterpret_cast<const float4*>(p + 64 * c + 16 * e);
     };
+    int t = blockIdx.x;
+    if (t >= ntiles) return;  // uniform over the workgroup
+    // the first tile's weights are requested before the hidden rows are
+    // ready (they do not depend on them), so HEAD's LayerNorm hides behind them
+    float4 wa[NCH][4], wb[NCH][4];
+    load(wa, t);
+    float4 hb[NCH][4];
+    if constexpr (HEAD) {
+        extern __shared__ float4 hs[];  // the normalised rows [rows][d / 4]
+        const int d4 = d >> 2;
+        for (int r = w; r < rows; r += 4) {
+            const float4* x4 = reinterpret_cast<const float4*>(h + (size_t)r * d);
+            float s = 0.0f, s2 = 0.0f, mean, rs;
+            for (int j = lane; j < d4; j += 64) ln_accum(x4[j], s, s2);
+            ln_finish(s, s2, d, ha.eps, mean, rs);
+            const float4* g4 = reinterpret_cast<const float4*>(ha.gamma);
+            const float4* b4 = reinterpret_cast<const float4*>(ha.beta);
+            for (int j = lane; j < d4; j += 64) hs[r * d4 + j] = ln_apply(x4[j], g4[j], b4[j], mean, rs);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                hb[c][e] = i < rows ? hs[i * d4 + ((kq + 64 * c + 16 * e + 4 * g) >> 2)]
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                hb[c][e] = i < rows ? *reinterpret_cast<const float4*>(h + (size_t)i * d + kq + 64 * c + 16 * e + 4 * g)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    // this lane's best logit of row i so far (wave 0, HEAD): indices only grow
+    // along a lane's walk, so a strict > keeps the first maximum
+    float best = -INFINITY;
+    int bi = INT_MAX;
     int par = 0;
     auto tile = [&](const float4 (&b)[NCH][4], int t) {
         f32x4 acc[4];
@@ -180,15 +240,18 @@ __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int vr = t * 16 + 4 * g + v;  // result row 4g + v, hidden row i
-                if (vr < V) logits[(size_t)i * V + vr] = s4[v];
+                if (vr < V) {
+                    logits[(size_t)i * V + vr] = s4[v];
+                    if constexpr (HEAD)
+                        if (s4[v] > best || bi == INT_MAX) {
+                            best = s4[v];
+                            bi = vr;
+                        }
+                }
             }
         }
         par ^= 1;
     };
-    int t = blockIdx.x;
-    if (t >= ntiles) return;  // uniform over the workgroup
-    float4 wa[NCH][4], wb[NCH][4];
-    load(wa, t);
     while (true) {
         load(wb, t + gridDim.x);
         tile(wa, t);
@@ -199,6 +262,29 @@ __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const
         t += gridDim.x;
         if (t >= ntiles) break;
     }
+    if constexpr (HEAD) {
+        if (w == 0) {
+            // lanes i, i + 16, i + 32, i + 48 hold row i's candidates
+            unsigned long long key = bi == INT_MAX ? 0ull : argmax_key(best, bi);
+#pragma unroll
+            for (int o = 16; o < 64; o <<= 1) {
+                const unsigned long long other = __shfl_xor(key, o, 64);
+                key = other > key ? other : key;
+            }
+            if (g == 0 && i < rows && key) atomicMax(ha.keys + i, key);
+        }
+    }
+}
+
+// The token ids of a fused head: tokens[b] = index held in keys[b], keys
+// cleared for the next step, positions[b] += 1 after a decode step.
+__global__ void head_finalize_kernel(int B, unsigned long long* __restrict__ keys, int* __restrict__ tokens,
+                                     int* __restrict__ positions, int advance) {
+    const int b = threadIdx.x;
+    if (b >= B) return;
+    tokens[b] = (int)(0xFFFFFFFFu - (uint32_t)keys[b]);
+    keys[b] = 0ull;
+    if (advance) positions[b] += 1;
 }
 
 // src/sampler.cu:10-14 on the device: first index of the maximum (ties go to
@@ -313,12 +399,13 @@ void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits
         // one workgroup per CU: more measured no faster (the stream is
         // bandwidth-bound with four waves' tiles in flight per CU)
         const unsigned grid = (unsigned)std::min<long long>((V + 15) / 16, num_cus());
+        const HeadArgs none{};
         switch (d / 256) {
-            case 1: vocab_proj_mfma_kernel<1><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
-            case 2: vocab_proj_mfma_kernel<2><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
-            case 3: vocab_proj_mfma_kernel<3><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
-            case 4: vocab_proj_mfma_kernel<4><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
-            default: vocab_proj_mfma_kernel<5><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V); break;
+            case 1: vocab_proj_mfma_kernel<1><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V, none); break;
+            case 2: vocab_proj_mfma_kernel<2><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V, none); break;
+            case 3: vocab_proj_mfma_kernel<3><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V, none); break;
+            case 4: vocab_proj_mfma_kernel<4><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V, none); break;
+            default: vocab_proj_mfma_kernel<5><<<grid, 256, 0, s>>>(rows, h, wte, logits, d, V, none); break;
         }
         return;
     }
@@ -327,6 +414,30 @@ void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits
         vocab_proj_kernel<1><<<blocks, 256, 0, s>>>(rows, h, wte, logits, d, V);
     else
         vocab_proj_kernel<16><<<blocks, 256, 0, s>>>(rows, h, wte, logits, d, V);
+}
+
+bool vocab_head_supported(int rows, int d) { return rows >= 1 && rows <= 16 && d % 256 == 0 && d <= 1024; }
+
+void launch_vocab_head(int rows, const float* x, const float* gamma, const float* beta, float eps,
+                       const float* wte, float* logits, int d, int V, unsigned long long* keys, hipStream_t s) {
+    HeadArgs ha;
+    ha.gamma = gamma;
+    ha.beta = beta;
+    ha.eps = eps;
+    ha.keys = keys;
+    const unsigned grid = (unsigned)std::min<long long>((V + 15) / 16, num_cus());
+    const size_t lds = (size_t)rows * d * sizeof(float);
+    switch (d / 256) {
+        case 1: vocab_proj_mfma_kernel<1, true><<<grid, 256, lds, s>>>(rows, x, wte, logits, d, V, ha); break;
+        case 2: vocab_proj_mfma_kernel<2, true><<<grid, 256, lds, s>>>(rows, x, wte, logits, d, V, ha); break;
+        case 3: vocab_proj_mfma_kernel<3, true><<<grid, 256, lds, s>>>(rows, x, wte, logits, d, V, ha); break;
+        default: vocab_proj_mfma_kernel<4, true><<<grid, 256, lds, s>>>(rows, x, wte, logits, d, V, ha); break;
+    }
+}
+
+void launch_head_finalize(int B, unsigned long long* keys, int* tokens, int* positions, bool advance,
+                          hipStream_t s) {
+    head_finalize_kernel<<<1, 64, 0, s>>>(B, keys, tokens, positions, advance ? 1 : 0);
 }
 
 void launch_argmax(int rows, const float* logits, int n, int* out, hipStream_t s) {

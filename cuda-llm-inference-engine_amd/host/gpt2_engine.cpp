@@ -284,6 +284,8 @@ struct GPT2Engine::Impl {
     int *block_table = nullptr, *positions = nullptr, *ctx_lens = nullptr, *tokens = nullptr;
     float* ws = nullptr;
     size_t ws_bytes = 0;
+    // fused head: per-row argmax keys [max_batch], zero between steps
+    unsigned long long* head_keys = nullptr;
     // Attention split plan of the current step (set by run_step): the
     // max_context_len and split count handed to the split kernel, as
     // ie_decode_attn would be called with them.
@@ -292,6 +294,7 @@ struct GPT2Engine::Impl {
     };
     AttnPlan plan;
     bool fused = false;  // fused step kernels apply to this model
+    bool qkv_attn = false;  // the fused step's one-launch QKV + attention applies
 
     int pos = 0;  // host mirror: tokens in every active sequence
     int* host_tokens = nullptr;  // pinned [max_batch]
@@ -420,8 +423,11 @@ struct GPT2Engine::Impl {
                     ie::gemv_fused_supported(m, d, ie::kSrcQuant, IE_EPI_BIAS_RESIDUAL) &&
                     ie::gemv_fused_supported(m, ff, ie::kSrcQuant, IE_EPI_BIAS_RESIDUAL) &&
                     ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, IE_EPI_PLAIN);
+        qkv_attn = fused && ie::qkv_attn_supported(d, cfg.n_heads, cfg.d_head, kBlock);
         HIPC(hipHostMalloc(&host_tokens, sizeof(int) * B));
         topk_buf = dev<float>(2 * ie::kTopkMax);
+        head_keys = dev<unsigned long long>(B);
+        HIPC(hipMemset(head_keys, 0, sizeof(unsigned long long) * B));
         HIPC(hipHostMalloc(&host_topk_buf, sizeof(float) * 2 * ie::kTopkMax));
         reset();
     }
@@ -463,8 +469,10 @@ struct GPT2Engine::Impl {
     }
 
     // The decode step with LayerNorm / quantizer prologues and the QKV-append
-    // epilogue: 6 launches per layer.  Same
-    // operations and order as enqueue_step_unfused.
+    // epilogue, and with a one-split attention plan the QKV projection and
+    // the attention in one launch per (sequence, head): 4 launches per layer
+    // (5 with more splits), plus the embedding and a two-launch head.  Same
+    // operations and order as enqueue_step_unfused, so the same bits.
     void enqueue_step_fused(int B) {
         const int d = cfg.d_model, H = cfg.n_heads;
         hipStream_t s = stream;
@@ -475,6 +483,16 @@ struct GPT2Engine::Impl {
             io.q = q; io.kc = layer_k(l); io.vc = layer_v(l); io.kv_dtype = opt.kv_dtype;
             io.positions = positions; io.table = block_table; io.nbps = nbps; io.block_size = kBlock;
             io.ctx_lens = ctx_lens;
+            if (plan.splits == 1 && qkv_attn) {
+                // QKV projection and attention in one launch per (sequence, head)
+                io.src = ie::kSrcLnQuant; io.x = x; io.gamma = L.ln1_g; io.beta = L.ln1_b; io.eps = 1e-5f;
+                ie::launch_qkv_attn(B, H, L.qkv.packed, L.qkv.scale, L.qkv_b, io, attn, s);
+                IEC(ie::check_launch("qkv_attn"));
+                fused_gemv(B, L.out, ie::kSrcQuant, attn, nullptr, nullptr, IE_EPI_BIAS_RESIDUAL, L.out_b, x, x);
+                fused_gemv(B, L.up, ie::kSrcLnQuant, x, L.ln2_g, L.ln2_b, IE_EPI_BIAS_GELU, L.up_b, nullptr, h);
+                fused_gemv(B, L.down, ie::kSrcQuant, h, nullptr, nullptr, IE_EPI_BIAS_RESIDUAL, L.down_b, x, x);
+                continue;
+            }
             fused_gemv(B, L.qkv, ie::kSrcLnQuant, x, L.ln1_g, L.ln1_b, ie::kEpiQKV, L.qkv_b, nullptr,
                        nullptr, &io);
             ie::DecodeArgs a{};
@@ -491,17 +509,24 @@ struct GPT2Engine::Impl {
             fused_gemv(B, L.up, ie::kSrcLnQuant, x, L.ln2_g, L.ln2_b, IE_EPI_BIAS_GELU, L.up_b, nullptr, h);
             fused_gemv(B, L.down, ie::kSrcQuant, h, nullptr, nullptr, IE_EPI_BIAS_RESIDUAL, L.down_b, x, x);
         }
-        enqueue_head(B);
-        ie::launch_advance(B, positions, s);
-        IEC(ie::check_launch("advance"));
+        enqueue_head(B, true);
     }
 
     // Final LayerNorm, LM head and argmax over the hidden rows x [B, d]
     // (src/gpt2_engine.cu:612-627, 391-410; sampler.cu:10-14): logits
-    // [B, V], argmax ids into `tokens`.
-    void enqueue_head(int B) {
+    // [B, V], argmax ids into `tokens`, and (advance, after a decode step)
+    // every position moved on.  The fused step with the fp32 head does it in
+    // two launches (LayerNorm + LM head + per-row argmax keys, then the ids).
+    void enqueue_head(int B, bool advance) {
         const int d = cfg.d_model, V = cfg.vocab_size;
         ie_stream_t st = (ie_stream_t)stream;
+        if (fused && !opt.int8_lm_head && ie::vocab_head_supported(B, d)) {
+            ie::launch_vocab_head(B, x, lnf_g, lnf_b, 1e-5f, wte, logits, d, V, head_keys, stream);
+            IEC(ie::check_launch("vocab_head"));
+            ie::launch_head_finalize(B, head_keys, tokens, positions, advance, stream);
+            IEC(ie::check_launch("head_finalize"));
+            return;
+        }
         if (fused) {
             if (opt.int8_lm_head) {
                 fused_gemv(B, head, ie::kSrcLnQuant, x, lnf_g, lnf_b, IE_EPI_PLAIN, nullptr, nullptr, logits);
@@ -520,6 +545,10 @@ struct GPT2Engine::Impl {
             }
         }
         IEC(ie_argmax(B, logits, V, tokens, st));
+        if (advance) {
+            ie::launch_advance(B, positions, stream);
+            IEC(ie::check_launch("advance"));
+        }
     }
 
     // One linear of the unfused step or of prefill over M rows:
@@ -570,9 +599,7 @@ struct GPT2Engine::Impl {
             linear(B, L.up, L.up_f, xn, IE_EPI_BIAS_GELU, L.up_b, nullptr, h, act_q, act_s, gemm_out);
             linear(B, L.down, L.down_f, h, IE_EPI_BIAS_RESIDUAL, L.down_b, x, x, act_q, act_s, gemm_out);
         }
-        enqueue_head(B);
-        ie::launch_advance(B, positions, s);
-        IEC(ie::check_launch("advance"));
+        enqueue_head(B, true);
     }
 
     // Split plan for a step whose attention sees ctx tokens: one split per
@@ -728,7 +755,7 @@ struct GPT2Engine::Impl {
                               sizeof(float) * d, B, hipMemcpyDeviceToDevice, stream));
         ie::launch_set_positions(B, pos, positions, ctx_lens, stream);
         IEC(ie::check_launch("set_positions"));
-        enqueue_head(B);
+        enqueue_head(B, false);
     }
 
     // Prompt of B sequences x P tokens through prefill (or, if disabled, one
