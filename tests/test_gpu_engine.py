@@ -351,19 +351,24 @@ def test_generate_uses_prefill_and_matches_stepwise_prompt(ie, mid_dir):
 EOS = 50256
 
 
-def echo_model(path, eos_from):
-    """Zero-weight model over the GPT-2 vocabulary (one layer, d 64): the
+def echo_cfg(d=64):
+    return dict(n_layers=1, n_heads=d // 64, d_model=d, d_ff=4 * d if d > 64 else 64, vocab_size=EOS + 1,
+                max_seq_len=128)
+
+
+def echo_model(path, eos_from, d=64):
+    """Zero-weight model over the GPT-2 vocabulary (one layer, width d): the
     final hidden row at position p is wte[t] + wpe[p].  wte rows are N(0, 1),
-    so LN(wte[t]) . wte[t] ~ 64 beats every other row (~8 per unit of
-    Gaussian tail, under 40 over 50k rows) and greedy decoding repeats its
-    input; from position eos_from on, wpe adds 20 wte[EOS] and <|endoftext|>
-    wins.  Returns the tensors."""
+    so LN(wte[t]) . wte[t] ~ d beats every other row (~sqrt(d) per unit of
+    Gaussian tail, under 5 sqrt(d) over 50k rows) and greedy decoding repeats
+    its input; from position eos_from on, wpe adds 20 wte[EOS] and
+    <|endoftext|> wins.  Returns the tensors."""
     from gpt2_model import random_tensors, write_model
 
-    cfg = dict(n_layers=1, n_heads=1, d_model=64, d_ff=64, vocab_size=EOS + 1, max_seq_len=128)
+    cfg = echo_cfg(d)
     t = random_tensors(cfg, 77, zero_weights=True, zero_biases=True, ln_jitter=0)
-    t["wte"] = np.random.default_rng(78).standard_normal((EOS + 1, 64)).astype(np.float32)
-    t["wpe"] = np.zeros((128, 64), np.float32)
+    t["wte"] = np.random.default_rng(78).standard_normal((EOS + 1, d)).astype(np.float32)
+    t["wpe"] = np.zeros((128, d), np.float32)
     t["wpe"][eos_from:] = 20 * t["wte"][EOS]
     write_model(str(path), cfg, t, fp32_weights=False)
     return t
@@ -456,3 +461,25 @@ def test_session_continuation_attends_to_the_cache(ie, mid_dir, prefill):
                 assert picks[p] == int(np.argmax(want)), p
                 checked += 1
     assert checked >= 6
+
+
+def test_greedy_ties_take_the_lowest_index(ie, tmp_path):
+    """Equal logits: the greedy token is the first index of the maximum
+    (src/sampler.cu:10-14, std::max_element), also in the fused head, which
+    merges per-workgroup maxima with a 64-bit atomic max.  The echo model with
+    wte rows 5001 and 40000 copies of row 5000 gives those three rows equal
+    logits whenever the input is any of them (rows 5000 and 5001 share a
+    16-row vocabulary tile; 40000 is in another workgroup's).  Width 768, so
+    the fused step and its fused head apply."""
+    from gpt2_model import write_model
+
+    t = echo_model(tmp_path / "base", 100, d=768)
+    t["wte"][5001] = t["wte"][5000]
+    t["wte"][40000] = t["wte"][5000]
+    write_model(str(tmp_path / "ties"), echo_cfg(768), t, fp32_weights=False)
+    prompts = np.array([[7, 40000], [9, 5001]], np.int32)
+    for kw in (dict(), dict(fuse=False), dict(use_graph=False)):
+        eng = ie.Engine(tmp_path / "ties", max_batch=2, **kw)
+        out, _ = eng.generate(prompts, 4, ignore_eos=True)
+        assert (out == 5000).all(), (kw, out)
+        eng.close()
