@@ -13,11 +13,15 @@
 //   * K advances 128 bytes per stage; a stage is 2 x 256 rows x 128 B = 64 KiB
 //     and two stages (128 KiB of the 160 KiB LDS) alternate: one stage's
 //     copies in flight while the other is read (four k-substeps of 32 B);
-//   * global -> LDS copies use global_load_lds_dwordx4 (16 B per lane straight
-//     into LDS, no VGPR round trip); a wave-load fills 1 KiB = 8 rows, the
-//     lane -> global address map applies the LDS swizzle, so the fixed
-//     lane-ordered LDS destination lands each 16-byte chunk at its swizzled
-//     slot;
+//   * global -> LDS copies go straight into LDS (16 B per lane, no VGPR round
+//     trip); a wave-load fills 1 KiB = 8 rows, the lane -> global address map
+//     applies the LDS swizzle, so the fixed lane-ordered LDS destination lands
+//     each 16-byte chunk at its swizzled slot.  Operands under 2 GiB use the
+//     buffer form (buffer_load_dwordx4 ... lds): a lane's 32-bit row offset is
+//     fixed for the whole K loop and the stage's K offset is one scalar, so a
+//     copy needs no per-stage address arithmetic (8192^3: 441.6 against 457.8
+//     us, same box, same bits); larger ones use global_load_lds_dwordx4 with
+//     64-bit addresses;
 //   * LDS rows are 128 B with 16-byte chunk c of row r stored at slot
 //     c ^ ((r >> 1) & 7) (swz), which spreads the rows an MFMA operand read
 //     touches over all banks;
@@ -64,6 +68,15 @@ __device__ __forceinline__ void load_rows(const int8_t* __restrict__ src, int ld
     __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)(lds_oper + r0 * BK), 16, 0, 0);
 }
 
+// The buffer form of load_rows: `voff` = the lane's byte offset of its row
+// and chunk (row clamped to the valid rows), `k0` the stage's K offset; the
+// descriptor covers the operand's `nbytes` (loads past it would read 0).
+__device__ __forceinline__ void load_rows_buf(const int8_t* src, uint32_t nbytes, uint32_t voff, int k0,
+                                              int8_t* lds_dst) {
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(src), 0, nbytes, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 16, voff, k0, 0, 0);
+}
+
 __device__ __forceinline__ i32x4 read_frag(const int8_t* lds_oper, int row, int chunk) {
     return *reinterpret_cast<const i32x4*>(lds_oper + row * BK + ((chunk ^ swz(row)) << 4));
 }
@@ -71,7 +84,8 @@ __device__ __forceinline__ i32x4 read_frag(const int8_t* lds_oper, int row, int 
 // NW = 4: 2 x 2 waves of 128 x 128 (one wave per SIMD); NW = 8: 2 x 4 waves
 // of 128 x 64 (two per SIMD, so one wave's MFMAs can run while the other
 // waits at the stage barrier or for its copies).
-template <int EPI, int NW>
+// BUF: M*K and N*K below 2^31, so operands take the buffer-form copies.
+template <int EPI, int NW, bool BUF>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     int M, int N, int K, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
@@ -110,6 +124,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     // Copies stage kt_src into LDS slot `slot`.  Every iteration issues one
     // stage, so the loop body is branch-free: past the last stage the copy
     // re-reads stage nk-1 into the slot just freed, which is never read again.
+    uint32_t voA[LOADS_PER_WAVE], voB[LOADS_PER_WAVE];
+    if constexpr (BUF) {
+#pragma unroll
+        for (int j = 0; j < LOADS_PER_WAVE; ++j) {
+            const int r = (wave * LOADS_PER_WAVE + j) * ROWS_PER_LOAD + lane / CHUNKS;
+            const int c = (lane % CHUNKS) ^ swz(r);
+            voA[j] = (uint32_t)(min(m0 + r, M - 1) * K + c * 16);
+            voB[j] = (uint32_t)(min(n0 + r, N - 1) * K + c * 16);
+        }
+    }
     auto issue = [&](int kt_src, int slot) {
         int8_t* sa = lds + slot * STAGE;
         int8_t* sb = sa + OPER;
@@ -117,8 +141,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
 #pragma unroll
         for (int j = 0; j < LOADS_PER_WAVE; ++j) {
             const int r0 = (wave * LOADS_PER_WAVE + j) * ROWS_PER_LOAD;
-            load_rows(A, K, M, m0, k0, r0, sa);
-            load_rows(BT, K, N, n0, k0, r0, sb);
+            if constexpr (BUF) {
+                load_rows_buf(A, (uint32_t)M * K, voA[j], k0, sa + r0 * BK);
+                load_rows_buf(BT, (uint32_t)N * K, voB[j], k0, sb + r0 * BK);
+            } else {
+                load_rows(A, K, M, m0, k0, r0, sa);
+                load_rows(BT, K, N, n0, k0, r0, sb);
+            }
         }
     };
     constexpr int LOADS_PER_STAGE = 2 * LOADS_PER_WAVE;  // per wave
@@ -208,7 +237,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     // and C may alias them).  Two waves per SIMD leave no room for all 64 row
     // scales beside the accumulators, so they are gathered one block at a time.
     // C goes out as non-temporal stores (2316 against 2187 TOP/s at 8192^3
-    // with the stores cached in L2).
+    // with the stores cached in L2; 16-byte stores of quad-transposed values
+    // measured no faster).
     const int h = lane >> 5;
     const int rbase = m0 + wm * 128 + 4 * h;
     const int cbase = n0 + wn * 32 * NJ + (lane & 31);
@@ -268,11 +298,17 @@ struct BigLaunch {
     static void run(const GemmArgs& a, hipStream_t s) {
         const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
         // 8 waves: 2231-2240 TOP/s steady state against 2153 with 4 (same box,
-        // bit-identical C)
+        // bit-identical C); with buffer-form copies 453.8 against 484.2 us.
         constexpr int NW = 8;
-        gemm_i8_256_kernel<EPI, NW><<<tm * tn, 64 * NW, 0, s>>>(
-            a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
-            a.sA, a.sB, a.bias, a.residual, a.C, tm, tn);
+        const bool buf = (long long)a.M * a.K < (1LL << 31) && (long long)a.N * a.K < (1LL << 31);
+        if (buf)
+            gemm_i8_256_kernel<EPI, NW, true><<<tm * tn, 64 * NW, 0, s>>>(
+                a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
+                a.sA, a.sB, a.bias, a.residual, a.C, tm, tn);
+        else
+            gemm_i8_256_kernel<EPI, NW, false><<<tm * tn, 64 * NW, 0, s>>>(
+                a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
+                a.sA, a.sB, a.bias, a.residual, a.C, tm, tn);
     }
 };
 

@@ -368,9 +368,13 @@ def test_big_tile_kernel_exact(ie, orc, M, N, K):
     assert np.array_equal(C[idx].cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("M,N", [(2304, 4100), (2300, 4100), (2300, 4099)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
-def test_big_tile_epilogues(ie, orc, epi):
-    M, N, K = 2304, 4100, 768
+def test_big_tile_epilogues(ie, orc, epi, M, N):
+    """Every epilogue on the 256x256-tile kernel: N % 4 == 0 takes the
+    quad-transposed 16-byte stores (full and ragged M), N % 4 != 0 the
+    per-element stores; rows from every 256-row tile edge and the ragged end."""
+    K = 768
     A, W = problem(M, N, K, 40 + epi)
     r = rng(41)
     bias = r.standard_normal(N).astype(np.float32)
@@ -379,7 +383,7 @@ def test_big_tile_epilogues(ie, orc, epi):
     Wp, sW = orc.quantize(W)
     got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi, dev(bias) if epi else None,
                             dev(res) if epi == 3 else None, path=ie.PATH_MFMA))
-    rows = [0, 1, 1000, 2303]
+    rows = sorted({0, 1, 2, 3, 5, 8, 31, 127, 128, 255, 256, 1000, 2047, 2048, M - 5, M - 2, M - 1})
     want = orc.gemm(Ap[rows], Wp, sA[rows], sW, epi, bias if epi else None, res[rows] if epi == 3 else None)
     if epi == 2:
         assert np.allclose(got[rows], want, rtol=2e-6, atol=1e-7)
