@@ -155,6 +155,119 @@ __device__ __forceinline__ void consume_chunk(const Chunk<D, KV, T>& c, const fl
 // chunks round-robin (this one is `wave`).  bt is the sequence's block-table
 // row.  On return every lane holds the wave's totals (o summed over the four
 // lane rows).
+//
+// SplitWalk holds a wave's walk in two parts: begin() issues the block-table
+// lookups and the first R - 1 chunks' loads, run() consumes the chunks with
+// the query slice it is given.  split_partial calls them back to back; the
+// engine's fused QKV + attention kernel issues begin() before its projection,
+// so those loads are in flight while the projection runs, and hands run() a
+// patch that substitutes the token it has just appended (held in LDS) for
+// that token's cache row, which the early loads may have read before it was
+// written.  The arithmetic and its order are the same either way.
+template <int D, int G, typename KV, int WPS, bool BS16, int R>
+struct SplitWalk {
+    static constexpr int EPL = D / 16;
+    // Chunk rows and ring depth: R chunks of 4T tokens cycle through the
+    // registers, R - 1 of them in flight while one is computed.
+    static constexpr int T = 4;            // lane rows hold T tokens each
+    static constexpr int CT = 4 * T;       // tokens per chunk
+    static constexpr int STEP = CT * WPS;  // tokens per round of the split's waves
+    static constexpr int NPH = (T + 3) / 4;  // blocks per chunk
+    // d = 128 bf16 rings keep their loads in place (measured 2-5% faster at
+    // ctx 4096-32768); fp32 rings need the register room sinking gives them
+    // and d = 64 bf16 measured 9% slower.
+    static constexpr bool OPQ = sizeof(KV) == 2 && D == 128;
+
+    Chunk<D, KV, T> buf[R];
+    int pn[NPH];
+    int c0, tok1, grp, block_size;
+    size_t tok_stride;
+    const KV* kbase;
+    const KV* vbase;
+    const int* bt;
+    bool any;
+
+    // With block size 16 a chunk lies in one block, so its physical block id
+    // is wave-uniform: it comes from a scalar load issued one chunk ahead
+    // (pn), which does not wait behind the in-flight KV loads as a vector
+    // load would (they retire in issue order), so the next KV loads go out as
+    // soon as a chunk is done.  Chunks past the end re-read the last token
+    // (masked), so every step issues the same loads and the ring needs no
+    // branches.
+    __device__ __forceinline__ int phys(int cs) const { return bt[min(cs, tok1 - 1) >> 4]; }
+    __device__ __forceinline__ void prefetch(int cs) {
+#pragma unroll
+        for (int k = 0; k < NPH; ++k) pn[k] = phys(cs + 16 * k);
+    }
+    __device__ __forceinline__ void next(Chunk<D, KV, T>& c, int cs) {
+        if constexpr (BS16) {
+            load_chunk16(c, cs, grp, tok1, pn, tok_stride, kbase, vbase);
+            prefetch(cs + STEP);
+        } else {
+            load_chunk(c, cs, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+        }
+    }
+
+    __device__ __forceinline__ void begin(const KV* __restrict__ kcache, const KV* __restrict__ vcache,
+                                          const int* __restrict__ bt_row, int kvh, int H_kv, int bs, int tok0,
+                                          int tok1_, int wave, int lane) {
+        const int li = lane & 15;
+        grp = lane >> 4;
+        tok1 = tok1_;
+        block_size = bs;
+        bt = bt_row;
+        tok_stride = (size_t)H_kv * D;
+        kbase = (OPQ ? opaque_global(kcache) : kcache) + (size_t)kvh * D + li * EPL;
+        vbase = (OPQ ? opaque_global(vcache) : vcache) + (size_t)kvh * D + li * EPL;
+        c0 = tok0 + wave * CT;
+        if constexpr (BS16) prefetch(c0);
+        any = c0 < tok1;
+        if (any) {
+#pragma unroll
+            for (int p = 0; p < R - 1; ++p) next(buf[p], c0 + p * STEP);
+        }
+    }
+
+    // q: this lane's slice of the G (scaled) query rows.  patch(chunk, cs)
+    // may rewrite a chunk starting at token cs before it is consumed.
+    template <class Patch>
+    __device__ __forceinline__ void run(const float (&q)[G][EPL], float (&m)[G], float (&l)[G],
+                                        float (&o)[G][EPL], Patch&& patch) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            m[g] = -INFINITY;
+            l[g] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
+        }
+        // Each step issues the chunk R - 1 rounds ahead into the buffer
+        // consumed last, then consumes the current one.
+        if (any) {
+            bool more = true;
+            while (more) {
+#pragma unroll
+                for (int u = 0; u < R; ++u) {
+                    if (more) {
+                        next(buf[(u + R - 1) % R], c0 + (R - 1) * STEP);
+                        patch(buf[u], c0);
+                        consume_chunk<D, G, KV, T>(buf[u], q, m, l, o);
+                        c0 += STEP;
+                        more = c0 < tok1;
+                    }
+                }
+            }
+        }
+        // The four lane rows share the wave's running max: plain sums merge
+        // them.
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            l[g] = sum_xor32(sum_xor16(l[g]));
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) o[g][e] = sum_xor32(sum_xor16(o[g][e]));
+        }
+    }
+};
+
 template <int D, int G, typename KV, int WPS, bool BS16, int R>
 __device__ __forceinline__ void split_partial(const float* __restrict__ Q, const KV* __restrict__ kcache,
                                               const KV* __restrict__ vcache, const int* __restrict__ bt,
@@ -162,53 +275,9 @@ __device__ __forceinline__ void split_partial(const float* __restrict__ Q, const
                                               int tok1, int wave, int lane, float qscale, float (&m)[G],
                                               float (&l)[G], float (&o)[G][D / 16]) {
     constexpr int EPL = D / 16;
-    // Chunk rows and ring depth: R chunks of 4T tokens cycle through the
-    // registers, R - 1 of them in flight while one is computed.  fp32 with
-    // d = 128 takes 8-token chunks so four fit where two 16-token ones did.
-    constexpr int T = 4;              // lane rows hold T tokens each
-    constexpr int CT = 4 * T;         // tokens per chunk
-    constexpr int STEP = CT * WPS;    // tokens per round of the split's waves
-    const int grp = lane >> 4, li = lane & 15;
-    const size_t tok_stride = (size_t)H_kv * D;
-    // d = 128 bf16 rings keep their loads in place (measured 2-5% faster at
-    // ctx 4096-32768); fp32 rings need the register room sinking gives them
-    // and d = 64 bf16 measured 9% slower.
-    constexpr bool OPQ = sizeof(KV) == 2 && D == 128;
-    const KV* kbase = (OPQ ? opaque_global(kcache) : kcache) + (size_t)kvh * D + li * EPL;
-    const KV* vbase = (OPQ ? opaque_global(vcache) : vcache) + (size_t)kvh * D + li * EPL;
-
-    // Each wave walks its chunks, keeping the next R - 1 chunks' loads in
-    // flight while it computes the current one.  With block size 16 a chunk
-    // lies in one block, so its physical block id is wave-uniform: it comes
-    // from a scalar load issued one chunk ahead (pn), which does not wait
-    // behind the in-flight KV loads as a vector load would (they retire in
-    // issue order), so the next KV loads go out as soon as a chunk is done.
-    // Chunks past the end re-read the last token (masked), so every step
-    // issues the same loads and the ring needs no branches.
-    Chunk<D, KV, T> buf[R];
-    int c0 = tok0 + wave * CT;
-    constexpr int NPH = (T + 3) / 4;  // blocks per chunk
-    auto phys = [&](int cs) { return bt[min(cs, tok1 - 1) >> 4]; };
-    int pn[NPH];
-    auto prefetch = [&](int cs) {
-#pragma unroll
-        for (int k = 0; k < NPH; ++k) pn[k] = phys(cs + 16 * k);
-    };
-    if constexpr (BS16) prefetch(c0);
-    auto next = [&](Chunk<D, KV, T>& c, int cs) {
-        if constexpr (BS16) {
-            load_chunk16(c, cs, grp, tok1, pn, tok_stride, kbase, vbase);
-            prefetch(cs + STEP);
-        } else {
-            load_chunk(c, cs, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
-        }
-    };
-    const bool any = c0 < tok1;
-    if (any) {
-#pragma unroll
-        for (int p = 0; p < R - 1; ++p) next(buf[p], c0 + p * STEP);
-    }
-
+    const int li = lane & 15;
+    SplitWalk<D, G, KV, WPS, BS16, R> w;
+    w.begin(kcache, vcache, bt, kvh, H_kv, block_size, tok0, tok1, wave, lane);
     float q[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -216,39 +285,7 @@ __device__ __forceinline__ void split_partial(const float* __restrict__ Q, const
 #pragma unroll
         for (int e = 0; e < EPL; ++e) q[g][e] *= qscale;
     }
-
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
-    }
-
-    // Each step issues the chunk R - 1 rounds ahead into the buffer consumed
-    // last, then consumes the current one.
-    if (any) {
-        while (true) {
-#pragma unroll
-            for (int u = 0; u < R; ++u) {
-                next(buf[(u + R - 1) % R], c0 + (R - 1) * STEP);
-                consume_chunk<D, G, KV, T>(buf[u], q, m, l, o);
-                c0 += STEP;
-                if (c0 >= tok1) goto done;
-            }
-        }
-    }
-done:
-
-    // The four lane rows share the wave's running max: plain sums merge them.
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        l[g] = sum_xor32(sum_xor16(l[g]));
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            o[g][e] = sum_xor32(sum_xor16(o[g][e]));
-        }
-    }
+    w.run(q, m, l, o, [](Chunk<D, KV, 4>&, int) {});
 }
 
 // End of a split shared by WPS > 1 waves: the waves' partials merged in

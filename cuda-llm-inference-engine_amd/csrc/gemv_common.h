@@ -79,7 +79,28 @@ __device__ __forceinline__ void gemv_store(void* C, int m, int n, int N, int32_t
 // quant.hip).  So the bytes equal those of the standalone LayerNorm +
 // quantizer pair, and do not depend on M or on which kernel stages the row.
 // Split into a load phase and a compute phase, so a wave can have several
-// rows' loads in flight before it computes any of them.
+// rows' loads in flight before it computes any of them.  The LayerNorm's
+// gamma/beta (the same for every row) are loaded with the first row
+// (ln_load), not after the row's mean and variance: that would be a second
+// memory round trip on the prologue's critical path.
+template <int K>
+struct LnVec {
+    float4 g[K / 256], b[K / 256];
+};
+
+template <int K, int SRC>
+__device__ __forceinline__ void ln_load(const GemvFusion& f, LnVec<K>& p, int lane) {
+    if constexpr (SRC == kSrcLnQuant) {
+        const float4* g4 = reinterpret_cast<const float4*>(f.gamma);
+        const float4* b4 = reinterpret_cast<const float4*>(f.beta);
+#pragma unroll
+        for (int i = 0; i < K / 256; ++i) {
+            p.g[i] = g4[lane + 64 * i];
+            p.b[i] = b4[lane + 64 * i];
+        }
+    }
+}
+
 template <int K>
 __device__ __forceinline__ void stage_load(const float* __restrict__ xr, float4 (&v)[K / 256], int lane) {
     static_assert(K % 256 == 0, "a lane stages whole float4s");
@@ -89,18 +110,16 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ xr, float4 
 }
 
 template <int K, int SRC>
-__device__ __forceinline__ void stage_compute(float4 (&v)[K / 256], const GemvFusion& f, int32_t* dst,
-                                              float* scale, int lane) {
+__device__ __forceinline__ void stage_compute(float4 (&v)[K / 256], const GemvFusion& f, const LnVec<K>& p,
+                                              int32_t* dst, float* scale, int lane) {
     constexpr int NV = K / 256;
     if constexpr (SRC == kSrcLnQuant) {
         float s = 0.0f, s2 = 0.0f, mean, rs;
 #pragma unroll
         for (int i = 0; i < NV; ++i) ln_accum(v[i], s, s2);
         ln_finish(s, s2, K, f.eps, mean, rs);
-        const float4* g4 = reinterpret_cast<const float4*>(f.gamma);
-        const float4* b4 = reinterpret_cast<const float4*>(f.beta);
 #pragma unroll
-        for (int i = 0; i < NV; ++i) v[i] = ln_apply(v[i], g4[lane + 64 * i], b4[lane + 64 * i], mean, rs);
+        for (int i = 0; i < NV; ++i) v[i] = ln_apply(v[i], p.g[i], p.b[i], mean, rs);
     }
     float mx = 0.0f;
 #pragma unroll
@@ -119,8 +138,10 @@ template <int K, int SRC>
 __device__ __forceinline__ void stage_row(const float* __restrict__ xr, const GemvFusion& f,
                                           int32_t* dst, float* scale, int lane) {
     float4 v[K / 256];
+    LnVec<K> p;
     stage_load<K>(xr, v, lane);
-    stage_compute<K, SRC>(v, f, dst, scale, lane);
+    ln_load<K, SRC>(f, p, lane);
+    stage_compute<K, SRC>(v, f, p, dst, scale, lane);
 }
 
 // Rows m >= M of a fused prologue: zero bytes (their outputs are not stored).

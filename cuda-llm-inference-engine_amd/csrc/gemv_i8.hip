@@ -249,6 +249,7 @@ __global__ __launch_bounds__(64 * NWV) void gemv_i8_mfma16_kernel(
         // (4 at K <= 1024, 2 at larger K for registers), so the rows cost one
         // memory round trip per batch, not one each.
         constexpr int RB = K <= 1024 ? 4 : 2;
+        LnVec<K> p;
 #pragma unroll
         for (int m0 = 0; m0 < 16; m0 += NWV * RB) {
             float4 v[RB][K / 256];
@@ -257,12 +258,13 @@ __global__ __launch_bounds__(64 * NWV) void gemv_i8_mfma16_kernel(
                 const int m = m0 + NWV * r + wave;
                 if (m < M) stage_load<K>(f.x + (size_t)m * K, v[r], lane);
             }
+            if (m0 == 0) ln_load<K, SRC>(f, p, lane);
 #pragma unroll
             for (int r = 0; r < RB; ++r) {
                 const int m = m0 + NWV * r + wave;
                 int32_t* dst = reinterpret_cast<int32_t*>(a_lds + m * (K / 16));
                 if (m < M)
-                    stage_compute<K, SRC>(v[r], f, dst, &s_sa[m], lane);
+                    stage_compute<K, SRC>(v[r], f, p, dst, &s_sa[m], lane);
                 else
                     zero_row<K>(dst, &s_sa[m], lane);
             }

@@ -6,14 +6,21 @@
 // QKV projection and the attention need no grid-wide step between them when
 // a workgroup owns the head's 3 x D projection rows.  The workgroup
 //   1. requests the head's 3 x D weight rows and their epilogue operands,
+//      and (SplitWalk::begin) the block-table lookups and first cache chunk
+//      of each wave's share of the attention, which are in flight during
+//      steps 2-3,
 //   2. builds the int8 activation row of x[b] in LDS (LayerNorm + per-row
 //      quantizer: stage_row, as the fused GEMV prologue),
 //   3. computes the rows with dot4 and the 16-lane DPP reduction and stores
 //      them as the QKV epilogue does: q to Q, k and v appended to the cache at
-//      the sequence's position (src/gpt2_engine.cu:464-481 of the reference),
-//   4. walks the head's cached tokens with split_partial on its 8 waves and
-//      merges them in LDS (split_finish_lds), as decode_attn_split_kernel does
-//      for a one-split plan (src/gpt2_engine.cu:496-504 / K13).
+//      the sequence's position (src/gpt2_engine.cu:464-481 of the reference);
+//      the head's q, k and v also go to LDS, in the cache's representation,
+//   4. walks the head's cached tokens on its 8 waves (SplitWalk::run) with q
+//      from LDS, substituting the LDS k and v for every read of the appended
+//      token's cache row (the early loads may have read it before it was
+//      written), and merges the waves in LDS (split_finish_lds), as
+//      decode_attn_split_kernel does for a one-split plan
+//      (src/gpt2_engine.cu:496-504 / K13).
 // Every value is produced by the same device code in the same order as the
 // QKV GEMV + attention kernel pair, so the outputs are bit-identical to that
 // pair (and to the step built from the C ABI).  One launch per layer fewer:
@@ -42,6 +49,8 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* 
     constexpr int d = kQaK;
     __shared__ i32x4 a_lds[K16];
     __shared__ float s_sa[1];
+    __shared__ float s_q[D];
+    __shared__ __attribute__((aligned(16))) KV s_k[D], s_v[D];
     const int h = blockIdx.x, b = blockIdx.y;
     const int lane = threadIdx.x & 63, li = lane & 15;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -73,6 +82,12 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* 
     size_t slot[1];
     qkv_slots<1>(fb, 1, slot);
 
+    // Tokens 0 .. pos of the sequence (never past its block-table row).
+    const int pos = f.positions[b];
+    const int tok1 = (int)min((long long)pos + 1, (long long)f.nbps * f.block_size);
+    SplitWalk<D, 1, KV, kQaWaves, true, 2> walk;
+    walk.begin(kcache, vcache, fb.table, h, H, f.block_size, 0, tok1, wv, lane);
+
     if (wv == 0) stage_row<kQaK, kSrcLnQuant>(f.x + (size_t)b * d, f, reinterpret_cast<int32_t*>(a_lds), &s_sa[0],
                                              lane);
     __syncthreads();
@@ -81,17 +96,49 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* 
         int32_t acc[1] = {0};
 #pragma unroll
         for (int t = 0; t < CPL; ++t) dot_chunk<1>(acc, wreg[g][t], a_lds, K16, li + 16 * t);
-        gemv_finish<1, kEpiQKV>(acc, li, row_of(g), true, 1, 3 * d, s_sa, ein[g], slot, nullptr, fb);
+        // gemv_finish<1, kEpiQKV>, plus the LDS copy of the stored value.
+        const int32_t tot = row16_sum(acc[0]);
+        if (li == 0) {
+            const int n = row_of(g);
+            gemv_store<kEpiQKV>(nullptr, 0, n, 3 * d, tot, s_sa[0], ein[g], slot[0], fb);
+            const float v = epilogue_value<IE_EPI_BIAS>(tot, s_sa[0], ein[g].sb, ein[g].bias, 0.0f);
+            const int lr = (wv * G + g) * 4 + (lane >> 4);
+            const int which = lr / D, r = lr - which * D;
+            if (which == 0) {
+                s_q[r] = v;
+            } else {
+                KV kv;
+                if constexpr (sizeof(KV) == 2)
+                    kv = f32_to_bf16_rne(v);
+                else
+                    kv = v;
+                (which == 1 ? s_k : s_v)[r] = kv;
+            }
+        }
     }
-    // The head's q and its new cache row are read back below.
     __syncthreads();
 
-    // Tokens 0 .. pos of the sequence (never past its block-table row).
-    const int ctx = f.positions[b] + 1;
-    const int tok1 = (int)min((long long)ctx, (long long)f.nbps * f.block_size);
-    float m[1], l[1], o[1][D / 16];
-    split_partial<D, 1, KV, kQaWaves, true, 2>(f.q, kcache, vcache, fb.table, b, h, H, H, f.block_size, 0, tok1,
-                                                wv, lane, qscale, m, l, o);
+    constexpr int EPL = D / 16;
+    float q[1][EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) q[0][e] = s_q[li * EPL + e] * qscale;
+    const int grp = lane >> 4;
+    auto patch = [&](Chunk<D, KV, 4>& c, int cs) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (min(cs + 4 * j + grp, tok1 - 1) == pos) {
+                const uint32_t* kw = reinterpret_cast<const uint32_t*>(s_k + li * EPL);
+                const uint32_t* vw = reinterpret_cast<const uint32_t*>(s_v + li * EPL);
+#pragma unroll
+                for (int w = 0; w < Slice<EPL, KV>::WORDS; ++w) {
+                    c.k[j].w[w] = kw[w];
+                    c.v[j].w[w] = vw[w];
+                }
+            }
+        }
+    };
+    float m[1], l[1], o[1][EPL];
+    walk.run(q, m, l, o, patch);
     split_finish_lds<D, 1, kQaWaves>(b, h, H, 0, 1, wv, lane, m, l, o, nullptr, O);
 }
 

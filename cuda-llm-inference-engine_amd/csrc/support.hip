@@ -175,7 +175,15 @@ __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const
 #pragma unroll
         for (int c = 0; c < NCH; ++c)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) b[c][e] = *reinterpret_cast<const float4*>(p + 64 * c + 16 * e);
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (HEAD)
+                {
+                    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 64 * c + 16 * e));
+                    b[c][e] = make_float4(v.x, v.y, v.z, v.w);
+                }
+                else
+                    b[c][e] = *reinterpret_cast<const float4*>(p + 64 * c + 16 * e);
+            }
     };
     int t = blockIdx.x;
     if (t >= ntiles) return;  // uniform over the workgroup

@@ -298,6 +298,11 @@ struct GPT2Engine::Impl {
 
     int pos = 0;  // host mirror: tokens in every active sequence
     int* host_tokens = nullptr;  // pinned [max_batch]
+    // Greedy decode keeps one step in flight ahead of the host (see
+    // GreedyPipe): each step's ids land in ring slot (step % 2), pinned
+    // [2][max_batch], and ring_ev[slot] marks their arrival.
+    int* host_ring = nullptr;
+    hipEvent_t ring_ev[2] = {nullptr, nullptr};
     // top-k sampler: k values then k indices in one device buffer
     // [2 kTopkMax words] and its pinned host copy (one transfer per token)
     float* topk_buf = nullptr;
@@ -425,6 +430,8 @@ struct GPT2Engine::Impl {
                     ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, IE_EPI_PLAIN);
         qkv_attn = fused && ie::qkv_attn_supported(d, cfg.n_heads, cfg.d_head, kBlock);
         HIPC(hipHostMalloc(&host_tokens, sizeof(int) * B));
+        HIPC(hipHostMalloc(&host_ring, sizeof(int) * 2 * B));
+        for (auto& e : ring_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         topk_buf = dev<float>(2 * ie::kTopkMax);
         head_keys = dev<unsigned long long>(B);
         HIPC(hipMemset(head_keys, 0, sizeof(unsigned long long) * B));
@@ -439,6 +446,9 @@ struct GPT2Engine::Impl {
         for (void* p : pf_allocs) (void)hipFree(p);
         if (pf.host_ids) (void)hipHostFree(pf.host_ids);
         if (host_tokens) (void)hipHostFree(host_tokens);
+        if (host_ring) (void)hipHostFree(host_ring);
+        for (auto& e : ring_ev)
+            if (e) (void)hipEventDestroy(e);
         if (host_topk_buf) (void)hipHostFree(host_topk_buf);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -652,6 +662,60 @@ struct GPT2Engine::Impl {
     void check_ids(const int* t, size_t n) const {
         if (ie_check_token_ids((int)n, t, cfg.vocab_size) != IE_OK) throw std::runtime_error(ie_last_error());
     }
+
+    // Whether the step at the current position would first have to capture
+    // its graph (done on an idle stream).
+    bool step_needs_capture(int B) const {
+        if (!opt.use_graph) return false;
+        auto it = graphs.find({B, plan_for(pos + 1).splits});
+        return it == graphs.end() || !it->second;
+    }
+
+    // Greedy decode with one step in flight ahead of the host: the argmax of
+    // a step is already in the device token buffer, where the next step's
+    // embedding reads it, so step k + 1 is enqueued before the host waits
+    // for step k's ids (copied to ring slot k % 2 behind step k; stream
+    // order puts the copy before step k + 1 overwrites the buffer).  The GPU
+    // then runs the steps back to back instead of idling for each host round
+    // trip.  launch() enqueues a step if the caller's limits allow one more
+    // (EOS, which only the host sees, is the one stop that cannot be known in
+    // advance); wait() returns the oldest in-flight step's ids; finish()
+    // undoes a step that was enqueued past the stop: the position mirror and
+    // the device positions go back one, and the device token buffer gets the
+    // ids the host kept (the cache row that step wrote is overwritten by the
+    // next step or prompt at that position).
+    struct GreedyPipe {
+        Impl& I;
+        int B;
+        long launched = 0, waited = 0;
+        GreedyPipe(Impl& impl, int b) : I(impl), B(b) {}
+        void launch() {
+            if (I.step_needs_capture(B)) HIPC(hipStreamSynchronize(I.stream));
+            I.run_step(B);
+            const int slot = (int)(launched & 1);
+            HIPC(hipMemcpyAsync(I.host_ring + slot * B, I.tokens, sizeof(int) * B, hipMemcpyDeviceToHost,
+                                I.stream));
+            HIPC(hipEventRecord(I.ring_ev[slot], I.stream));
+            ++launched;
+        }
+        const int* wait() {
+            const int slot = (int)(waited & 1);
+            HIPC(hipEventSynchronize(I.ring_ev[slot]));
+            ++waited;
+            return I.host_ring + slot * B;
+        }
+        void finish(const int* last_ids) {
+            if (launched == waited) return;
+            HIPC(hipStreamSynchronize(I.stream));
+            I.pos -= (int)(launched - waited);
+            ie::launch_set_positions(B, I.pos, I.positions, I.ctx_lens, I.stream);
+            IEC(ie::check_launch("set_positions"));
+            std::memcpy(I.host_tokens, last_ids, sizeof(int) * B);
+            HIPC(hipMemcpyAsync(I.tokens, I.host_tokens, sizeof(int) * B, hipMemcpyHostToDevice, I.stream));
+            HIPC(hipStreamSynchronize(I.stream));
+            waited = launched;
+        }
+    };
 
     // Upload one token per sequence, run a step, fetch the argmax ids.
     void step_tokens(const int* toks, int B, bool fetch) {
@@ -910,17 +974,41 @@ void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tok
 
     std::vector<float> itl;
     float decode_ms = 0.0f;
-    for (int stepi = 0; stepi < max_new_tokens; ++stepi) {
-        if (next == 50256) break;  // GPT-2 <|endoftext|>, src/gpt2_engine.cu:717
-        token_callback(next);
-        metrics.tokens_generated = stepi + 1;
-        if (I.pos >= I.cfg.max_seq_len) break;
-        const auto t = Clock::now();
-        I.step_tokens(&next, 1, greedy);
-        next = pick();
-        const float dt = ms_since(t);
-        itl.push_back(dt);
-        decode_ms += dt;
+    if (greedy) {
+        // The same loop with the next step enqueued before the host reads the
+        // current one (GreedyPipe): the argmax is already on the device.
+        // As the loop below, every emitted token is fed through a step (the
+        // last one's result is not emitted).
+        Impl::GreedyPipe pipe(I, 1);
+        auto t = Clock::now();
+        if (max_new_tokens > 0 && I.pos < I.cfg.max_seq_len) pipe.launch();
+        for (int stepi = 0; stepi < max_new_tokens; ++stepi) {
+            if (next == 50256) break;  // GPT-2 <|endoftext|>, src/gpt2_engine.cu:717
+            token_callback(next);
+            metrics.tokens_generated = stepi + 1;
+            if (pipe.launched == pipe.waited) break;  // context full
+            if (stepi + 1 < max_new_tokens && I.pos < I.cfg.max_seq_len) pipe.launch();
+            next = *pipe.wait();
+            const auto now = Clock::now();
+            const float dt = std::chrono::duration<float, std::milli>(now - t).count();
+            t = now;
+            itl.push_back(dt);
+            decode_ms += dt;
+        }
+        pipe.finish(&next);
+    } else {
+        for (int stepi = 0; stepi < max_new_tokens; ++stepi) {
+            if (next == 50256) break;  // GPT-2 <|endoftext|>, src/gpt2_engine.cu:717
+            token_callback(next);
+            metrics.tokens_generated = stepi + 1;
+            if (I.pos >= I.cfg.max_seq_len) break;
+            const auto t = Clock::now();
+            I.step_tokens(&next, 1, greedy);
+            next = pick();
+            const float dt = ms_since(t);
+            itl.push_back(dt);
+            decode_ms += dt;
+        }
     }
     I.fill_tail_metrics(metrics, itl, decode_ms, 1, (long)itl.size());
     metrics.end_to_end_ms = ms_since(t_total);
@@ -952,27 +1040,37 @@ void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, in
     float decode_ms = 0.0f;
     std::vector<char> done(B, 0);
     long decode_tokens = 0;
+    // The argmax of the previous step is already in the device token buffer:
+    // each step reads it directly, only the ids come back, and the next step
+    // is enqueued before the host waits for the current one (GreedyPipe).
+    Impl::GreedyPipe pipe(I, B);
+    std::vector<int> cur(I.host_tokens, I.host_tokens + B);
+    auto t = Clock::now();
+    if (max_new_tokens > 1 && I.pos < I.cfg.max_seq_len) pipe.launch();
     for (int stepi = 0; stepi < max_new_tokens; ++stepi) {
         bool all_done = true;
         for (int b = 0; b < B; ++b) {
-            const int tkn = I.host_tokens[b];
+            const int tkn = cur[b];
             if (!done[b] && !ignore_eos && tkn == 50256) done[b] = 1;
             if (!done[b]) out[b].push_back(tkn);
             all_done = all_done && done[b];
         }
         metrics.tokens_generated = stepi + 1;
-        if (all_done || stepi + 1 == max_new_tokens || I.pos >= I.cfg.max_seq_len) break;
-        // The argmax of the previous step is already in the device token
-        // buffer: the step reads it directly, only the ids come back.
+        // The step for this iteration was enqueued unless a limit other than
+        // EOS ruled it out: stop here as the step-by-step loop would.
+        if (all_done || pipe.launched == pipe.waited) break;
         for (int b = 0; b < B; ++b) decode_tokens += done[b] ? 0 : 1;
-        const auto t = Clock::now();
-        I.run_step(B);
-        HIPC(hipMemcpyAsync(I.host_tokens, I.tokens, sizeof(int) * B, hipMemcpyDeviceToHost, I.stream));
-        HIPC(hipStreamSynchronize(I.stream));
-        const float dt = ms_since(t);
+        if (stepi + 2 < max_new_tokens && I.pos < I.cfg.max_seq_len) pipe.launch();
+        const int* ids = pipe.wait();
+        std::copy(ids, ids + B, cur.begin());
+        const auto now = Clock::now();
+        const float dt = std::chrono::duration<float, std::milli>(now - t).count();
+        t = now;
         itl.push_back(dt);
         decode_ms += dt;
     }
+    pipe.finish(cur.data());
+    std::copy(cur.begin(), cur.end(), I.host_tokens);
     I.fill_tail_metrics(metrics, itl, decode_ms, B, decode_tokens);
     metrics.end_to_end_ms = ms_since(t_total);
     metrics.generating = false;
