@@ -52,21 +52,21 @@ constexpr int kChunk = 128;  // 16-byte columns of A per LDS chunk (2 KiB of K)
 // NT: weight loads are non-temporal (streamed past the caches).  Used for
 // weight matrices too large to stay cache-resident between calls; measured
 // 10% faster at K = 8192, N = 28672.
-template <int MT, int EPI, int K16, int SRC = kSrcInt8, bool NT = false>
-__global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
+template <int MT, int EPI, int K16, int SRC = kSrcInt8, bool NT = false, int GF = 0, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void gemv_i8_fixed_kernel(
     int M, int N, const int32_t* __restrict__ A, const int32_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
     const float* residual, void* C, GemvFusion f) {
     constexpr int CPL = K16 / 16;                             // chunks per lane per row
-    constexpr int G = CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;   // row groups per pass
+    constexpr int G = GF > 0 ? GF : CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;   // row groups per pass
     static_assert(CPL <= 32, "fixed-K GEMV covers K <= 8192");
-    static_assert(SRC == kSrcInt8 || MT <= 4, "one staging wave per row");
+    static_assert(SRC == kSrcInt8 || MT <= NW, "one staging wave per row");
     __shared__ i32x4 a_lds[MT * K16];
     __shared__ float s_sa[MT];
     const int lane = threadIdx.x & 63;
     const int li = lane & 15;
-    const int wave_global = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int step = gridDim.x * 4 * (4 * G);
+    const int wave_global = blockIdx.x * NW + (threadIdx.x >> 6);
+    const int step = gridDim.x * NW * (4 * G);
     const i32x4* w4 = reinterpret_cast<const i32x4*>(BT);
 
     i32x4 wv[G][CPL];
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void gemv_i8_fixed_kernel(
 
     if constexpr (SRC == kSrcInt8) {
         const i32x4* a4 = reinterpret_cast<const i32x4*>(A);
-        for (int i = threadIdx.x; i < MT * K16; i += 256) {
+        for (int i = threadIdx.x; i < MT * K16; i += 64 * NW) {
             const int m = i / K16;
             const int mm = m < M ? m : M - 1;
             a_lds[i] = a4[(size_t)mm * K16 + (i - m * K16)];
@@ -722,11 +722,11 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
 // (a quarter of the 256 MiB MALL: larger ones do not stay resident anyway).
 constexpr size_t kStreamWeightBytes = 64ull << 20;
 
-template <int MT, int EPI, int K16, int SRC = kSrcInt8>
+template <int MT, int EPI, int K16, int SRC = kSrcInt8, int GF = 0, int NW = 4>
 void launch_fixed(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFusion{}) {
     constexpr int CPL = K16 / 16;
-    constexpr int G = CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;
-    const int rows_per_wg = 4 * 4 * G;
+    constexpr int G = GF > 0 ? GF : CPL >= 12 ? 1 : (12 + CPL - 1) / CPL;
+    const int rows_per_wg = NW * 4 * G;
     const bool nt = (size_t)a.N * K16 * 16 >= kStreamWeightBytes;
     // Streaming shapes: one workgroup per CU walking row groups (each wave
     // keeps a whole group's loads in flight); measured faster than one
@@ -735,10 +735,10 @@ void launch_fixed(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFu
     const int cap = nt ? num_cus() : 2048;
     const unsigned blocks = (unsigned)min((a.N + rows_per_wg - 1) / rows_per_wg, cap);
     if (nt)
-        gemv_i8_fixed_kernel<MT, EPI, K16, SRC, true><<<blocks, 256, 0, s>>>(
+        gemv_i8_fixed_kernel<MT, EPI, K16, SRC, true, GF, NW><<<blocks, 64 * NW, 0, s>>>(
             a.M, a.N, a.A, a.BT, a.sA, a.sB, a.bias, a.residual, a.C, f);
     else
-        gemv_i8_fixed_kernel<MT, EPI, K16, SRC, false><<<blocks, 256, 0, s>>>(
+        gemv_i8_fixed_kernel<MT, EPI, K16, SRC, false, GF, NW><<<blocks, 64 * NW, 0, s>>>(
             a.M, a.N, a.A, a.BT, a.sA, a.sB, a.bias, a.residual, a.C, f);
 }
 
@@ -807,9 +807,14 @@ void launch_burst(const GemmArgs& a, hipStream_t s) {
     else go(std::integral_constant<int, 4>{});
 }
 
+// One decode row (M = 1): 16 rows per workgroup (one group of 4 rows per
+// wave) and, at K = 3072, one-wave workgroups, so more CUs share the few
+// hundred KB of weights and each wave's dot and epilogue chain is shorter
+// (GPT-2 Small batch-1 decode step 272 -> 252 us; 64 rows per 4-wave
+// workgroup before).
 template <int EPI, int K, int SRC>
 void launch_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s) {
-    if (a.M <= 1) launch_fixed<1, EPI, K / 16, SRC>(a, s, f);
+    if (a.M <= 1) launch_fixed<1, EPI, K / 16, SRC, 1, (K == 3072 ? 1 : 4)>(a, s, f);
     else if (a.M <= 2) launch_fixed<2, EPI, K / 16, SRC>(a, s, f);
     else if (a.M <= 4) launch_fixed<4, EPI, K / 16, SRC>(a, s, f);
     else launch_mfma16<EPI, K / 64, SRC>(a, s, f);

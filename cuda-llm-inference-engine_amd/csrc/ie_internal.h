@@ -60,12 +60,19 @@ struct GemvFusion {
     int nbps = 0;
     int block_size = 16;
     int* ctx_lens = nullptr;
+    // launch_qkv_attn only: with ids set, row m of x is not read but built
+    // as wte[ids[m]] + wpe[positions[m]] (the embedding, same arithmetic as
+    // embedding_batch_kernel) and stored to x.
+    const int* ids = nullptr;
+    const float* wte = nullptr;
+    const float* wpe = nullptr;
 };
 // The engine's QKV projection + decode attention in one launch, one
 // workgroup per (sequence, head) (qkv_attn.hip): f as for the kEpiQKV GEMV
 // with src kSrcLnQuant (x, LayerNorm gamma/beta), a one-split plan; O [B, d]
 // receives the attention output.  Bit-identical to launch_gemv_fused(QKV)
-// followed by launch_decode_attn with one split.
+// followed by launch_decode_attn with one split (with f.ids set, to the
+// embedding kernel followed by those two).
 bool qkv_attn_supported(int d_model, int n_heads, int d_head, int block_size);
 void launch_qkv_attn(int B, int H, const int32_t* BT, const float* sB, const float* bias, const GemvFusion& f,
                      float* O, hipStream_t s);

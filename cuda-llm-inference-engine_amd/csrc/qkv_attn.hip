@@ -10,7 +10,7 @@
 //      of each wave's share of the attention, which are in flight during
 //      steps 2-3,
 //   2. builds the int8 activation row of x[b] in LDS (LayerNorm + per-row
-//      quantizer: stage_row, as the fused GEMV prologue),
+//      quantizer, as the fused GEMV prologue; its loads go out in step 1),
 //   3. computes the rows with dot4 and the 16-lane DPP reduction and stores
 //      them as the QKV epilogue does: q to Q, k and v appended to the cache at
 //      the sequence's position (src/gpt2_engine.cu:464-481 of the reference);
@@ -25,6 +25,8 @@
 // QKV GEMV + attention kernel pair, so the outputs are bit-identical to that
 // pair (and to the step built from the C ABI).  One launch per layer fewer:
 // GPT-2 Small, d = 768, D = 64, block size 16, a one-split plan.
+#include <type_traits>
+
 #include "attn_split.h"
 #include "gemv_common.h"
 #include "ie_internal.h"
@@ -35,7 +37,10 @@ namespace {
 constexpr int kQaWaves = 8;  // the 8-wave form of the one-split attention
 constexpr int kQaK = 768;    // d_model (the projection's K)
 
-template <int D, typename KV>
+// EMB: the first layer's launch builds x[b] itself (f.ids set): the
+// embedding wte[ids[b]] + wpe[positions[b]], which head 0's workgroup also
+// stores to x for the layer's residual adds; the embedding launch is saved.
+template <int D, typename KV, bool EMB>
 __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* __restrict__ BT,
                                                                  const float* __restrict__ sB,
                                                                  const float* __restrict__ bias, GemvFusion f,
@@ -79,6 +84,32 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* 
 #pragma unroll
         for (int t = 0; t < CPL; ++t) wreg[g][t] = w[16 * t];
     }
+    // Wave 0's activation row and LayerNorm parameters are requested before
+    // the position / block-table lookups below: those are scalar loads in a
+    // dependent chain, and a wait for any scalar load waits for all of them.
+    float4 xv[kQaK / 256];
+    LnVec<kQaK> lnp;
+    if (wv == 0) {
+        if constexpr (EMB) {
+            const float4* e4 = reinterpret_cast<const float4*>(f.wte + (size_t)f.ids[b] * d);
+            const float4* p4 = reinterpret_cast<const float4*>(f.wpe + (size_t)f.positions[b] * d);
+            float4 ev[kQaK / 256], pv[kQaK / 256];
+#pragma unroll
+            for (int i = 0; i < kQaK / 256; ++i) {
+                ev[i] = e4[lane + 64 * i];
+                pv[i] = p4[lane + 64 * i];
+            }
+            ln_load<kQaK, kSrcLnQuant>(f, lnp, lane);
+#pragma unroll
+            for (int i = 0; i < kQaK / 256; ++i) {
+                xv[i] = make_float4(ev[i].x + pv[i].x, ev[i].y + pv[i].y, ev[i].z + pv[i].z, ev[i].w + pv[i].w);
+                if (h == 0) reinterpret_cast<float4*>(const_cast<float*>(f.x) + (size_t)b * d)[lane + 64 * i] = xv[i];
+            }
+        } else {
+            stage_load<kQaK>(f.x + (size_t)b * d, xv, lane);
+            ln_load<kQaK, kSrcLnQuant>(f, lnp, lane);
+        }
+    }
     size_t slot[1];
     qkv_slots<1>(fb, 1, slot);
 
@@ -88,8 +119,7 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* 
     SplitWalk<D, 1, KV, kQaWaves, true, 2> walk;
     walk.begin(kcache, vcache, fb.table, h, H, f.block_size, 0, tok1, wv, lane);
 
-    if (wv == 0) stage_row<kQaK, kSrcLnQuant>(f.x + (size_t)b * d, f, reinterpret_cast<int32_t*>(a_lds), &s_sa[0],
-                                             lane);
+    if (wv == 0) stage_compute<kQaK, kSrcLnQuant>(xv, f, lnp, reinterpret_cast<int32_t*>(a_lds), &s_sa[0], lane);
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -153,12 +183,20 @@ void launch_qkv_attn(int B, int H, const int32_t* BT, const float* sB, const flo
     constexpr int D = 64;
     const float qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
     const dim3 grid(H, B);
-    if (f.kv_dtype == IE_KV_BF16)
-        qkv_attn_kernel<D, uint16_t><<<grid, 64 * kQaWaves, 0, s>>>(
-            BT, sB, bias, f, static_cast<const uint16_t*>(f.kc), static_cast<const uint16_t*>(f.vc), H, qscale, O);
+    auto go = [&](auto emb) {
+        constexpr bool E = decltype(emb)::value;
+        if (f.kv_dtype == IE_KV_BF16)
+            qkv_attn_kernel<D, uint16_t, E><<<grid, 64 * kQaWaves, 0, s>>>(
+                BT, sB, bias, f, static_cast<const uint16_t*>(f.kc), static_cast<const uint16_t*>(f.vc), H, qscale,
+                O);
+        else
+            qkv_attn_kernel<D, float, E><<<grid, 64 * kQaWaves, 0, s>>>(
+                BT, sB, bias, f, static_cast<const float*>(f.kc), static_cast<const float*>(f.vc), H, qscale, O);
+    };
+    if (f.ids)
+        go(std::true_type{});
     else
-        qkv_attn_kernel<D, float><<<grid, 64 * kQaWaves, 0, s>>>(
-            BT, sB, bias, f, static_cast<const float*>(f.kc), static_cast<const float*>(f.vc), H, qscale, O);
+        go(std::false_type{});
 }
 
 }  // namespace ie

@@ -486,7 +486,10 @@ struct GPT2Engine::Impl {
     void enqueue_step_fused(int B) {
         const int d = cfg.d_model, H = cfg.n_heads;
         hipStream_t s = stream;
-        IEC(ie_embedding_batch(B, tokens, positions, d, wte, wpe, x, (ie_stream_t)s));
+        // With a one-split plan the first layer's QKV + attention launch
+        // builds the embedding itself.
+        const bool emb_fused = plan.splits == 1 && qkv_attn;
+        if (!emb_fused) IEC(ie_embedding_batch(B, tokens, positions, d, wte, wpe, x, (ie_stream_t)s));
         for (int l = 0; l < cfg.n_layers; ++l) {
             const Layer& L = layers[l];
             ie::GemvFusion io{};
@@ -496,6 +499,7 @@ struct GPT2Engine::Impl {
             if (plan.splits == 1 && qkv_attn) {
                 // QKV projection and attention in one launch per (sequence, head)
                 io.src = ie::kSrcLnQuant; io.x = x; io.gamma = L.ln1_g; io.beta = L.ln1_b; io.eps = 1e-5f;
+                if (l == 0 && emb_fused) { io.ids = tokens; io.wte = wte; io.wpe = wpe; }
                 ie::launch_qkv_attn(B, H, L.qkv.packed, L.qkv.scale, L.qkv_b, io, attn, s);
                 IEC(ie::check_launch("qkv_attn"));
                 fused_gemv(B, L.out, ie::kSrcQuant, attn, nullptr, nullptr, IE_EPI_BIAS_RESIDUAL, L.out_b, x, x);
