@@ -285,14 +285,20 @@ __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const
 }
 
 // The token ids of a fused head: tokens[b] = index held in keys[b], keys
-// cleared for the next step, positions[b] += 1 after a decode step.
+// cleared for the next step, positions[b] += 1 after a decode step.  With
+// host_ids (pinned host memory, [2][B]) the ids also go to slot
+// positions[b] & 1 there, the slot of the position the step processed, with
+// system-scope stores: the host reads them after the step without a copy.
 __global__ void head_finalize_kernel(int B, unsigned long long* __restrict__ keys, int* __restrict__ tokens,
-                                     int* __restrict__ positions, int advance) {
+                                     int* __restrict__ positions, int advance, int* host_ids) {
     const int b = threadIdx.x;
     if (b >= B) return;
-    tokens[b] = (int)(0xFFFFFFFFu - (uint32_t)keys[b]);
+    const int tok = (int)(0xFFFFFFFFu - (uint32_t)keys[b]);
+    tokens[b] = tok;
     keys[b] = 0ull;
-    if (advance) positions[b] += 1;
+    const int p = positions[b];
+    if (host_ids) __hip_atomic_store(host_ids + (p & 1) * B + b, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (advance) positions[b] = p + 1;
 }
 
 // src/sampler.cu:10-14 on the device: first index of the maximum (ties go to
@@ -444,8 +450,8 @@ void launch_vocab_head(int rows, const float* x, const float* gamma, const float
 }
 
 void launch_head_finalize(int B, unsigned long long* keys, int* tokens, int* positions, bool advance,
-                          hipStream_t s) {
-    head_finalize_kernel<<<1, 64, 0, s>>>(B, keys, tokens, positions, advance ? 1 : 0);
+                          int* host_ids, hipStream_t s) {
+    head_finalize_kernel<<<1, 64, 0, s>>>(B, keys, tokens, positions, advance ? 1 : 0, host_ids);
 }
 
 void launch_argmax(int rows, const float* logits, int n, int* out, hipStream_t s) {

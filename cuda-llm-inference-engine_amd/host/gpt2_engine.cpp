@@ -299,8 +299,9 @@ struct GPT2Engine::Impl {
     int pos = 0;  // host mirror: tokens in every active sequence
     int* host_tokens = nullptr;  // pinned [max_batch]
     // Greedy decode keeps one step in flight ahead of the host (see
-    // GreedyPipe): each step's ids land in ring slot (step % 2), pinned
-    // [2][max_batch], and ring_ev[slot] marks their arrival.
+    // GreedyPipe): each step's ids land in ring slot (position % 2), pinned
+    // [2][max_batch] (written by the fused head's finalize kernel, else
+    // copied), and ring_ev[slot] marks their arrival.
     int* host_ring = nullptr;
     hipEvent_t ring_ev[2] = {nullptr, nullptr};
     // top-k sampler: k values then k indices in one device buffer
@@ -430,7 +431,7 @@ struct GPT2Engine::Impl {
                     ie::gemv_fused_supported(m, d, ie::kSrcLnQuant, IE_EPI_PLAIN);
         qkv_attn = fused && ie::qkv_attn_supported(d, cfg.n_heads, cfg.d_head, kBlock);
         HIPC(hipHostMalloc(&host_tokens, sizeof(int) * B));
-        HIPC(hipHostMalloc(&host_ring, sizeof(int) * 2 * B));
+        HIPC(hipHostMalloc(&host_ring, sizeof(int) * 2 * B, hipHostMallocCoherent));
         for (auto& e : ring_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         topk_buf = dev<float>(2 * ie::kTopkMax);
         head_keys = dev<unsigned long long>(B);
@@ -531,13 +532,19 @@ struct GPT2Engine::Impl {
     // [B, V], argmax ids into `tokens`, and (advance, after a decode step)
     // every position moved on.  The fused step with the fp32 head does it in
     // two launches (LayerNorm + LM head + per-row argmax keys, then the ids).
+    // Whether the step's head is the fused one, whose finalize kernel also
+    // writes the ids to host_ring.
+    bool head_writes_host(int B) const {
+        return fused && !opt.int8_lm_head && ie::vocab_head_supported(B, cfg.d_model);
+    }
+
     void enqueue_head(int B, bool advance) {
         const int d = cfg.d_model, V = cfg.vocab_size;
         ie_stream_t st = (ie_stream_t)stream;
-        if (fused && !opt.int8_lm_head && ie::vocab_head_supported(B, d)) {
+        if (head_writes_host(B)) {
             ie::launch_vocab_head(B, x, lnf_g, lnf_b, 1e-5f, wte, logits, d, V, head_keys, stream);
             IEC(ie::check_launch("vocab_head"));
-            ie::launch_head_finalize(B, head_keys, tokens, positions, advance, stream);
+            ie::launch_head_finalize(B, head_keys, tokens, positions, advance, host_ring, stream);
             IEC(ie::check_launch("head_finalize"));
             return;
         }
@@ -692,18 +699,21 @@ struct GPT2Engine::Impl {
         Impl& I;
         int B;
         long launched = 0, waited = 0;
+        int slots[2] = {0, 0};  // ring slot of each in-flight step, oldest first
         GreedyPipe(Impl& impl, int b) : I(impl), B(b) {}
         void launch() {
             if (I.step_needs_capture(B)) HIPC(hipStreamSynchronize(I.stream));
+            const int slot = I.pos & 1;
             I.run_step(B);
-            const int slot = (int)(launched & 1);
-            HIPC(hipMemcpyAsync(I.host_ring + slot * B, I.tokens, sizeof(int) * B, hipMemcpyDeviceToHost,
-                                I.stream));
+            if (!I.head_writes_host(B))
+                HIPC(hipMemcpyAsync(I.host_ring + slot * B, I.tokens, sizeof(int) * B, hipMemcpyDeviceToHost,
+                                    I.stream));
             HIPC(hipEventRecord(I.ring_ev[slot], I.stream));
+            slots[launched & 1] = slot;
             ++launched;
         }
         const int* wait() {
-            const int slot = (int)(waited & 1);
+            const int slot = slots[waited & 1];
             HIPC(hipEventSynchronize(I.ring_ev[slot]));
             ++waited;
             return I.host_ring + slot * B;
