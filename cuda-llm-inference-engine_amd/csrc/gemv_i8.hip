@@ -339,7 +339,9 @@ __global__ __launch_bounds__(64 * NWV) void gemv_i8_mfma16_kernel(
 // their int32 tiles in LDS (exact), and each wave has at most one group (the
 // launcher sizes the grid so).  KS = 1: waves walk groups g, g + 8 gridDim.x,
 // ... and store each as it completes.
-template <int EPI, bool NT, int R>
+// MR: activation rows staged (8 when M <= 8: LDS rows 8-15 then hold
+// whatever they held, and only feed results that are not stored).
+template <int EPI, bool NT, int R, int MR = 16>
 __global__ __launch_bounds__(512) void gemv_i8_slice_kernel(int M, int N, int ks_log, const int8_t* __restrict__ A,
                                                             const int8_t* __restrict__ BT,
                                                             const float* __restrict__ sA,
@@ -377,11 +379,12 @@ __global__ __launch_bounds__(512) void gemv_i8_slice_kernel(int M, int N, int ks
 
     // Issue order: activation rows, row scales, then the ring's first R
     // batches; loads retire in order, so the LDS stores below wait only for
-    // the rows.
-    i32x4 stage[16];
+    // the rows.  Rows past M repeat row M - 1 (never stored): unconditional
+    // loads, which a conditional one per row would serialise (each branch
+    // waited for its load).
+    i32x4 stage[MR];
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-        if (j < M) stage[j] = reinterpret_cast<const i32x4*>(A + (size_t)j * K)[threadIdx.x];
+    for (int j = 0; j < MR; ++j) stage[j] = reinterpret_cast<const i32x4*>(A + (size_t)min(j, M - 1) * K)[threadIdx.x];
     float sa[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) sa[v] = EPI != IE_EPI_I32 ? sA[min(4 * kq + v, M - 1)] : 0.0f;
@@ -395,8 +398,7 @@ __global__ __launch_bounds__(512) void gemv_i8_slice_kernel(int M, int N, int ks
         for (int u = 0; u < U; ++u) w[r][u] = ldw(p + u * 64);
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-        if (j < M) reinterpret_cast<i32x4*>(a_lds + j * LDA)[threadIdx.x] = stage[j];
+    for (int j = 0; j < MR; ++j) reinterpret_cast<i32x4*>(a_lds + j * LDA)[threadIdx.x] = stage[j];
     __syncthreads();
 
     auto finish = [&](int g, const i32x4& acc) {
@@ -519,11 +521,14 @@ __global__ __launch_bounds__(512) void gemv_i8_parted_kernel(int M, int N, const
     auto out_n = [&](int t) { return 4 * (i0 + t * stride) + f; };
 
     // Issue order: activation rows, the first item's weights, its epilogue
-    // operands; the LDS stores wait only for the rows.
+    // operands; the LDS stores wait only for the rows.  Rows past M repeat
+    // row M - 1 (never used for a stored result): unconditional loads, which
+    // a conditional one per row would serialise (each branch waited for its
+    // load: N = K = 8192, M = 4 12.43 -> 11.95 us).
     i32x4 stage[4 * MB];
 #pragma unroll
     for (int j = 0; j < 4 * MB; ++j)
-        if (j < M) stage[j] = reinterpret_cast<const i32x4*>(A + (size_t)j * K)[threadIdx.x];
+        stage[j] = reinterpret_cast<const i32x4*>(A + (size_t)min(j, M - 1) * K)[threadIdx.x];
     i32x4 w[R][U];
     {
         const int8_t* p = wrow(0);
@@ -535,8 +540,7 @@ __global__ __launch_bounds__(512) void gemv_i8_parted_kernel(int M, int N, const
     const float sa = EPI != IE_EPI_I32 ? sA[m_c] : 0.0f;
     EpiIn e = epi_load<EPI>(m_c, min(out_n(0), N - 1), N, sB, bias, residual);
 #pragma unroll
-    for (int j = 0; j < 4 * MB; ++j)
-        if (j < M) reinterpret_cast<i32x4*>(a_lds + j * LDA)[threadIdx.x] = stage[j];
+    for (int j = 0; j < 4 * MB; ++j) reinterpret_cast<i32x4*>(a_lds + j * LDA)[threadIdx.x] = stage[j];
     __syncthreads();
 
     // A operand of block j: activation row 4 j + f (clamped to M - 1; those
@@ -769,7 +773,8 @@ void launch_slice(const GemmArgs& a, hipStream_t s) {
     const unsigned blocks = ks_log == 0 ? (unsigned)std::min(groups, cus) : (unsigned)((groups << ks_log) + 7) / 8;
     const bool nt = (size_t)a.N * 8192 >= kStreamWeightBytes;
     // a ring of 2 sets of 8 loads: measured level with 4 sets
-    auto* k = nt ? gemv_i8_slice_kernel<EPI, true, 2> : gemv_i8_slice_kernel<EPI, false, 2>;
+    auto* k = a.M <= 8 ? (nt ? gemv_i8_slice_kernel<EPI, true, 2, 8> : gemv_i8_slice_kernel<EPI, false, 2, 8>)
+                       : (nt ? gemv_i8_slice_kernel<EPI, true, 2> : gemv_i8_slice_kernel<EPI, false, 2>);
     k<<<blocks, 512, 0, s>>>(a.M, a.N, ks_log, reinterpret_cast<const int8_t*>(a.A),
                              reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
 }
