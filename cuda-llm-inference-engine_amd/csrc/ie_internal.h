@@ -186,15 +186,15 @@ void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits
                        int d, int V, hipStream_t s);
 // The decode step's head in one launch (support.hip): final LayerNorm of the
 // rows x [rows, d] (the standalone LayerNorm's bits), fp32 LM head over wte
-// into logits [rows, V], and each row's first-maximum index merged into
-// keys[row] (cleared to 0 beforehand); launch_head_finalize then writes the
-// token ids, clears the keys and (advance) moves the positions on; with
-// host_ids (pinned [2][B]) the ids also land in slot positions[b] & 1 there.
+// into logits [rows, V], each row's first-maximum index merged into
+// keys[row], and the last workgroup (counter `done`) writes the token ids,
+// clears keys and counter (both 0 before the first launch) and (advance)
+// moves the positions on; with host_ids (pinned [2][B]) the ids also land in
+// slot positions[b] & 1 there.
 bool vocab_head_supported(int rows, int d);
 void launch_vocab_head(int rows, const float* x, const float* gamma, const float* beta, float eps,
-                       const float* wte, float* logits, int d, int V, unsigned long long* keys, hipStream_t s);
-void launch_head_finalize(int B, unsigned long long* keys, int* tokens, int* positions, bool advance,
-                          int* host_ids, hipStream_t s);
+                       const float* wte, float* logits, int d, int V, unsigned long long* keys, unsigned* done,
+                       int* tokens, int* positions, bool advance, int* host_ids, hipStream_t s);
 void launch_argmax(int rows, const float* logits, int n, int* out,
                    hipStream_t s);
 

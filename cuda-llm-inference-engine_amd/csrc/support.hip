@@ -147,14 +147,37 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
 // same lane order, so the same bits), and the argmax of each row (first index
 // of the maximum) is folded in: every workgroup keeps its rows' best (value,
 // index) while it writes the logits and merges it into keys[row] with one
-// 64-bit atomic max (argmax_key); head_finalize_kernel turns the keys into
-// token ids.
+// 64-bit atomic max (argmax_key).  The last workgroup to finish (a counter,
+// `done`) turns the keys into token ids (finalize_row): every
+// workgroup's atomic max has completed (vmcnt) before its counter increment,
+// and keys and counter are only touched by atomics, so the last one to
+// increment reads every row's final key.  It then clears keys and counter
+// for the next launch.
 struct HeadArgs {
     const float* gamma = nullptr;
     const float* beta = nullptr;
     float eps = 1e-5f;
     unsigned long long* keys = nullptr;
+    unsigned* done = nullptr;  // 0 before the launch, 0 after it
+    int* tokens = nullptr;
+    int* positions = nullptr;
+    int advance = 0;
+    int* host_ids = nullptr;
 };
+
+// tokens[b] from keys[b] (cleared), the ids also to host_ids slot
+// positions[b] & 1 (system-scope stores; pinned host memory [2][B]), and
+// positions[b] += advance.
+__device__ __forceinline__ void finalize_row(int B, int b, unsigned long long* keys, int* tokens, int* positions,
+                                             int advance, int* host_ids) {
+    const unsigned long long k = __hip_atomic_load(keys + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int tok = (int)(0xFFFFFFFFu - (uint32_t)k);
+    tokens[b] = tok;
+    __hip_atomic_store(keys + b, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int p = positions[b];
+    if (host_ids) __hip_atomic_store(host_ids + (p & 1) * B + b, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (advance) positions[b] = p + 1;
+}
 
 template <int NCH, bool HEAD = false>
 __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const float* __restrict__ h,
@@ -281,24 +304,20 @@ __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const
             }
             if (g == 0 && i < rows && key) atomicMax(ha.keys + i, key);
         }
+        __shared__ int last;
+        if (threadIdx.x == 0) {
+            // wave 0's atomic maxima have completed before the increment
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            const unsigned prev = __hip_atomic_fetch_add(ha.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = prev == gridDim.x - 1;
+        }
+        __syncthreads();
+        if (last) {
+            if (threadIdx.x < rows)
+                finalize_row(rows, threadIdx.x, ha.keys, ha.tokens, ha.positions, ha.advance, ha.host_ids);
+            if (threadIdx.x == 0) __hip_atomic_store(ha.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
-}
-
-// The token ids of a fused head: tokens[b] = index held in keys[b], keys
-// cleared for the next step, positions[b] += 1 after a decode step.  With
-// host_ids (pinned host memory, [2][B]) the ids also go to slot
-// positions[b] & 1 there, the slot of the position the step processed, with
-// system-scope stores: the host reads them after the step without a copy.
-__global__ void head_finalize_kernel(int B, unsigned long long* __restrict__ keys, int* __restrict__ tokens,
-                                     int* __restrict__ positions, int advance, int* host_ids) {
-    const int b = threadIdx.x;
-    if (b >= B) return;
-    const int tok = (int)(0xFFFFFFFFu - (uint32_t)keys[b]);
-    tokens[b] = tok;
-    keys[b] = 0ull;
-    const int p = positions[b];
-    if (host_ids) __hip_atomic_store(host_ids + (p & 1) * B + b, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    if (advance) positions[b] = p + 1;
 }
 
 // src/sampler.cu:10-14 on the device: first index of the maximum (ties go to
@@ -433,12 +452,18 @@ void launch_vocab_proj(int rows, const float* h, const float* wte, float* logits
 bool vocab_head_supported(int rows, int d) { return rows >= 1 && rows <= 16 && d % 256 == 0 && d <= 1024; }
 
 void launch_vocab_head(int rows, const float* x, const float* gamma, const float* beta, float eps,
-                       const float* wte, float* logits, int d, int V, unsigned long long* keys, hipStream_t s) {
+                       const float* wte, float* logits, int d, int V, unsigned long long* keys, unsigned* done,
+                       int* tokens, int* positions, bool advance, int* host_ids, hipStream_t s) {
     HeadArgs ha;
     ha.gamma = gamma;
     ha.beta = beta;
     ha.eps = eps;
     ha.keys = keys;
+    ha.done = done;
+    ha.tokens = tokens;
+    ha.positions = positions;
+    ha.advance = advance ? 1 : 0;
+    ha.host_ids = host_ids;
     const unsigned grid = (unsigned)std::min<long long>((V + 15) / 16, num_cus());
     const size_t lds = (size_t)rows * d * sizeof(float);
     switch (d / 256) {
@@ -449,10 +474,6 @@ void launch_vocab_head(int rows, const float* x, const float* gamma, const float
     }
 }
 
-void launch_head_finalize(int B, unsigned long long* keys, int* tokens, int* positions, bool advance,
-                          int* host_ids, hipStream_t s) {
-    head_finalize_kernel<<<1, 64, 0, s>>>(B, keys, tokens, positions, advance ? 1 : 0, host_ids);
-}
 
 void launch_argmax(int rows, const float* logits, int n, int* out, hipStream_t s) {
     if (rows == 0) return;

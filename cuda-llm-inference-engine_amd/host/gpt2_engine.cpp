@@ -286,6 +286,7 @@ struct GPT2Engine::Impl {
     size_t ws_bytes = 0;
     // fused head: per-row argmax keys [max_batch], zero between steps
     unsigned long long* head_keys = nullptr;
+    unsigned* head_done = nullptr;  // the fused head's finishing-workgroup counter
     // Attention split plan of the current step (set by run_step): the
     // max_context_len and split count handed to the split kernel, as
     // ie_decode_attn would be called with them.
@@ -436,6 +437,8 @@ struct GPT2Engine::Impl {
         topk_buf = dev<float>(2 * ie::kTopkMax);
         head_keys = dev<unsigned long long>(B);
         HIPC(hipMemset(head_keys, 0, sizeof(unsigned long long) * B));
+        head_done = dev<unsigned>(1);
+        HIPC(hipMemset(head_done, 0, sizeof(unsigned)));
         HIPC(hipHostMalloc(&host_topk_buf, sizeof(float) * 2 * ie::kTopkMax));
         reset();
     }
@@ -542,10 +545,9 @@ struct GPT2Engine::Impl {
         const int d = cfg.d_model, V = cfg.vocab_size;
         ie_stream_t st = (ie_stream_t)stream;
         if (head_writes_host(B)) {
-            ie::launch_vocab_head(B, x, lnf_g, lnf_b, 1e-5f, wte, logits, d, V, head_keys, stream);
+            ie::launch_vocab_head(B, x, lnf_g, lnf_b, 1e-5f, wte, logits, d, V, head_keys, head_done, tokens,
+                                  positions, advance, host_ring, stream);
             IEC(ie::check_launch("vocab_head"));
-            ie::launch_head_finalize(B, head_keys, tokens, positions, advance, host_ring, stream);
-            IEC(ie::check_launch("head_finalize"));
             return;
         }
         if (fused) {
