@@ -534,9 +534,9 @@ struct GPT2Engine::Impl {
     // (src/gpt2_engine.cu:612-627, 391-410; sampler.cu:10-14): logits
     // [B, V], argmax ids into `tokens`, and (advance, after a decode step)
     // every position moved on.  The fused step with the fp32 head does it in
-    // two launches (LayerNorm + LM head + per-row argmax keys, then the ids).
-    // Whether the step's head is the fused one, whose finalize kernel also
-    // writes the ids to host_ring.
+    // one launch (LayerNorm + LM head + per-row argmax keys; its last
+    // workgroup writes the ids, also into host_ring).
+    // Whether the step's head is that fused one.
     bool head_writes_host(int B) const {
         return fused && !opt.int8_lm_head && ie::vocab_head_supported(B, cfg.d_model);
     }
