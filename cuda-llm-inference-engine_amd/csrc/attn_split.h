@@ -208,9 +208,11 @@ struct SplitWalk {
         }
     }
 
+    // pn0 >= 0: the physical block of the wave's first chunk, already loaded
+    // by the caller (block size 16 only); otherwise begin() looks it up.
     __device__ __forceinline__ void begin(const KV* __restrict__ kcache, const KV* __restrict__ vcache,
                                           const int* __restrict__ bt_row, int kvh, int H_kv, int bs, int tok0,
-                                          int tok1_, int wave, int lane) {
+                                          int tok1_, int wave, int lane, int pn0 = -1) {
         const int li = lane & 15;
         grp = lane >> 4;
         tok1 = tok1_;
@@ -220,7 +222,13 @@ struct SplitWalk {
         kbase = (OPQ ? opaque_global(kcache) : kcache) + (size_t)kvh * D + li * EPL;
         vbase = (OPQ ? opaque_global(vcache) : vcache) + (size_t)kvh * D + li * EPL;
         c0 = tok0 + wave * CT;
-        if constexpr (BS16) prefetch(c0);
+        if constexpr (BS16) {
+            static_assert(NPH == 1, "a chunk lies in one block");
+            if (pn0 >= 0)
+                pn[0] = pn0;
+            else
+                prefetch(c0);
+        }
         any = c0 < tok1;
         if (any) {
 #pragma unroll
@@ -273,11 +281,11 @@ __device__ __forceinline__ void split_partial(const float* __restrict__ Q, const
                                               const KV* __restrict__ vcache, const int* __restrict__ bt,
                                               int b, int kvh, int H_q, int H_kv, int block_size, int tok0,
                                               int tok1, int wave, int lane, float qscale, float (&m)[G],
-                                              float (&l)[G], float (&o)[G][D / 16]) {
+                                              float (&l)[G], float (&o)[G][D / 16], int pn0 = -1) {
     constexpr int EPL = D / 16;
     const int li = lane & 15;
     SplitWalk<D, G, KV, WPS, BS16, R> w;
-    w.begin(kcache, vcache, bt, kvh, H_kv, block_size, tok0, tok1, wave, lane);
+    w.begin(kcache, vcache, bt, kvh, H_kv, block_size, tok0, tok1, wave, lane, pn0);
     float q[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {

@@ -323,6 +323,15 @@ __global__ __launch_bounds__(NT) void decode_attn_split_kernel(
     const int wave = WPS == 1 ? 0 : wid;
     const int grp = lane >> 4, li = lane & 15;
 
+    const int* bt = block_table + (size_t)b * nbps;
+    // Block size 16: the wave's first chunk is block split * blocks_per_split
+    // + wave of the row whenever the split is not empty, so its id is loaded
+    // together with the context length instead of after it (one scalar
+    // round trip fewer before the first KV load; clamped into the row, and
+    // unused, for an empty split).
+    int pn0 = -1;
+    if constexpr (BS16)
+        if (nbps > 0) pn0 = bt[(int)min((long long)split * blocks_per_split + wave, (long long)nbps - 1)];
     const int ctx = context_lens[b];
     const long long span = (long long)blocks_per_split * block_size;
     const long long t0l = (long long)split * span;
@@ -332,10 +341,9 @@ __global__ __launch_bounds__(NT) void decode_attn_split_kernel(
     const int tok0 = (int)min(t0l, lim);
     const int tok1 = (int)min(t0l + span, lim);
 
-    const int* bt = block_table + (size_t)b * nbps;
     float m[G], l[G], o[G][EPL];
     split_partial<D, G, KV, WPS, BS16, R>(Q, kcache, vcache, bt, b, kvh, H_q, H_kv, block_size, tok0, tok1,
-                                       wave, lane, qscale, m, l, o);
+                                       wave, lane, qscale, m, l, o, pn0);
     // The partial of this split; an empty split writes o = 0, m = -inf, l = 0.
     // With a single split the partial is the result: O = o / l, written
     // directly with the merge's arithmetic (a merge of one split has weight
