@@ -122,10 +122,19 @@ __global__ __launch_bounds__(256) void vocab_proj_kernel(int rows, const float* 
 //     of 64.  It holds its quarter of the hidden rows in registers for the
 //     whole kernel, so nothing is staged per tile, and its partial 16 x 16
 //     tile is summed with the other three in LDS in a fixed order.
-//   * Within chunk c, load e of lane (i, g) (i = l % 16, g = l / 16) reads
-//     vocabulary row v0 + i at k = 64c + 16e + 4g .. +3, so the four lane
-//     groups of a row read 64 contiguous bytes; MFMA step (e, s) sums
-//     k = 64c + 16e + 4g + s over g for A and B alike, every k once.
+//   * MFMA operand layout: within chunk c, fragment e of lane (i, g)
+//     (i = l % 16, g = l / 16) is vocabulary row v0 + i at k = 64c + 16e +
+//     4g .. +3; MFMA step (e, s) sums k = 64c + 16e + 4g + s over g for A
+//     and B alike, every k once.
+//   * Loads: read in that layout, a wave instruction would cover 16 rows x
+//     64 bytes, half of each 128-byte line, and non-temporal loads then
+//     fetch every line twice (a streaming lab over the 154 MB GPT-2 wte:
+//     5.3 TB/s against 6.6 TB/s for whole lines).  So instruction (rg, c)
+//     reads rows 4rg .. 4rg + 3 x 256 contiguous bytes (lane l: row 4rg +
+//     l / 16, k = 64c + 4(l % 16)), and each wave passes its 12 fragments
+//     through its own 12 KB of LDS into the operand layout (XOR-swizzled
+//     slots: both the writes and the reads of 16 consecutive lanes cover 256
+//     distinct bytes).  The MFMAs see the same values in the same order.
 //   * Four accumulators (one per e) keep the MFMAs independent and are added
 //     in a fixed order.
 // A logit depends on its own hidden row only (zero columns add nothing to
@@ -180,12 +189,13 @@ __device__ __forceinline__ void finalize_row(int B, int b, unsigned long long* k
 }
 
 template <int NCH, bool HEAD = false>
-__global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const float* __restrict__ h,
+__global__ __launch_bounds__(256, NCH >= 5 ? 1 : 2) void vocab_proj_mfma_kernel(int rows, const float* __restrict__ h,
                                                                  const float* __restrict__ wte,
                                                                  float* __restrict__ logits, int d, int V,
                                                                  HeadArgs ha) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     __shared__ f32x4 red[2][4][64];
+    __shared__ f32x4 tr[4][4 * NCH][64];  // each wave's fragments on their way to the operand layout
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i = lane & 15, g = lane >> 4;
     const int kq = w * NCH * 64;
@@ -193,26 +203,45 @@ __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const
     // provenance hidden, so the compiler keeps the first tile's loads where
     // they are issued instead of sinking them past the LayerNorm to their use
     const float* wsrc = HEAD ? opaque_global(wte) : wte;
-    auto load = [&](float4 (&b)[NCH][4], int t) {
-        const float* p = wsrc + (size_t)min(min(t, ntiles - 1) * 16 + i, V - 1) * d + kq + 4 * g;
+    // b[rg][c]: row 4rg + l / 16, k = kq + 64c + 4(l % 16)
+    auto load = [&](f32x4 (&b)[4][NCH], int t) {
+        const int r0 = min(t, ntiles - 1) * 16 + (lane >> 4);
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+            const float* p = wsrc + (size_t)min(r0 + 4 * rg, V - 1) * d + kq + 4 * (lane & 15);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                if constexpr (HEAD)
+                    b[rg][c] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 64 * c));
+                else
+                    b[rg][c] = *reinterpret_cast<const f32x4*>(p + 64 * c);
+            }
+        }
+    };
+    // Slot of fragment (row 4rg + r4, k = 64c + 16e + 4g) in block (rg, c)
+    // of the wave's LDS: 16e + 4(r4 ^ e) + (g ^ rg).
+    auto to_operands = [&](const f32x4 (&b)[4][NCH], float4 (&a)[NCH][4]) {
+        {
+            const int r4 = lane >> 4, e = (lane >> 2) & 3, gg = lane & 3;
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) tr[w][rg * NCH + c][16 * e + 4 * (r4 ^ e) + (gg ^ rg)] = b[rg][c];
+        }
+        const int rg = i >> 2, r4 = i & 3;
 #pragma unroll
         for (int c = 0; c < NCH; ++c)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                if constexpr (HEAD)
-                {
-                    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 64 * c + 16 * e));
-                    b[c][e] = make_float4(v.x, v.y, v.z, v.w);
-                }
-                else
-                    b[c][e] = *reinterpret_cast<const float4*>(p + 64 * c + 16 * e);
+                const f32x4 v = tr[w][rg * NCH + c][16 * e + 4 * (r4 ^ e) + (g ^ rg)];
+                a[c][e] = make_float4(v.x, v.y, v.z, v.w);
             }
     };
     int t = blockIdx.x;
     if (t >= ntiles) return;  // uniform over the workgroup
     // the first tile's weights are requested before the hidden rows are
     // ready (they do not depend on them), so HEAD's LayerNorm hides behind them
-    float4 wa[NCH][4], wb[NCH][4];
+    f32x4 wa[4][NCH], wb[4][NCH];
     load(wa, t);
     float4 hb[NCH][4];
     if constexpr (HEAD) {
@@ -247,7 +276,9 @@ __global__ __launch_bounds__(256, 2) void vocab_proj_mfma_kernel(int rows, const
     float best = -INFINITY;
     int bi = INT_MAX;
     int par = 0;
-    auto tile = [&](const float4 (&b)[NCH][4], int t) {
+    auto tile = [&](const f32x4 (&raw)[4][NCH], int t) {
+        float4 b[NCH][4];
+        to_operands(raw, b);
         f32x4 acc[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
