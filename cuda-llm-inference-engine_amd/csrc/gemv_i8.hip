@@ -197,12 +197,25 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
 // C[4 * (l / 16) + v][n0 + l % 16].  The activation block is staged in LDS
 // (or built there by the fused prologue); weight loads run U steps ahead of
 // the MFMAs.
-template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false, int NWV = 4>
+template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false, int NWV = 4, int RS = 16>
 __global__ __launch_bounds__(64 * NWV) void gemv_i8_mfma16_kernel(
     int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
     const float* residual, void* C, GemvFusion f) {
     constexpr int K = K64 * 64;
+    // Workgroup (x, y) takes rows y RS .. y RS + RS - 1 (the MFMA tile keeps
+    // 16 rows; rows past the workgroup's are never stored, and a row's sums
+    // do not depend on the others, so every split gives the same bits).
+    if constexpr (RS < 16) {
+        static_assert(EPI != kEpiQKV, "QKV rows carry cache slots");
+        const int m0 = blockIdx.y * RS;
+        M = min(M - m0, RS);
+        if (A) A += (size_t)m0 * K;
+        if (sA) sA += m0;
+        if (residual) residual += (size_t)m0 * N;
+        C = static_cast<char*>(C) + (size_t)m0 * N * 4;
+        if (f.x) f.x += (size_t)m0 * K;
+    }
     static_assert(K64 % NWV == 0, "the waves split K evenly");
     static_assert(K <= 4096, "the activation block fits LDS");
     constexpr int KW = K64 / NWV;  // K steps per wave
@@ -725,6 +738,10 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(
 // Weight matrices at least this large are streamed with non-temporal loads
 // (a quarter of the 256 MiB MALL: larger ones do not stay resident anyway).
 constexpr size_t kStreamWeightBytes = 64ull << 20;
+// The 16-row MFMA GEMV splits its rows over several workgroups only for
+// weights up to this size: each row block re-reads the weights, which for
+// these stay in the caches.
+constexpr size_t kRowSplitWeightBytes = 8ull << 20;
 
 template <int MT, int EPI, int K16, int SRC = kSrcInt8, int GF = 0, int NW = 4>
 void launch_fixed(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvFusion{}) {
@@ -755,10 +772,22 @@ void launch_mfma16(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvF
     // M = 16, N = 768 GEMV 0.048 -> 0.055 of HBM peak, GPT-2 batch-16 decode
     // 30088 -> 30684 tok/s; K = 768 (12 steps) keeps 4.
     constexpr int NWV = (K64 % 8 == 0 && K64 >= 32) ? 8 : 4;
-    auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true, NWV> : gemv_i8_mfma16_kernel<EPI, K64, SRC, false, NWV>;
-    k<<<blocks, 64 * NWV, 0, s>>>(a.M, a.N, reinterpret_cast<const int8_t*>(a.A),
-                             reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual,
-                             a.C, f);
+    // Rows per workgroup: 4 when the weights stay cached (each row block
+    // re-reads them): a workgroup then stages 4 activation rows, not 16, and
+    // a CU keeps only so many bytes in flight (GPT-2 batch-16 decode step
+    // 413.7 -> 368.7 us, same bits; 1, 2 and 8 rows measured slower).  QKV
+    // epilogue rows carry cache slots and keep 16.
+    auto go = [&](auto rsc) {
+        constexpr int RS = decltype(rsc)::value;
+        auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true, NWV, RS>
+                     : gemv_i8_mfma16_kernel<EPI, K64, SRC, false, NWV, RS>;
+        k<<<dim3(blocks, (unsigned)((a.M + RS - 1) / RS)), 64 * NWV, 0, s>>>(
+            a.M, a.N, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB,
+            a.bias, a.residual, a.C, f);
+    };
+    if constexpr (EPI != kEpiQKV)
+        if ((size_t)a.N * K64 * 64 <= kRowSplitWeightBytes) return go(std::integral_constant<int, 4>{});
+    go(std::integral_constant<int, 16>{});
 }
 
 template <int EPI>
@@ -813,13 +842,15 @@ void launch_burst(const GemmArgs& a, hipStream_t s) {
 }
 
 // One decode row (M = 1): 16 rows per workgroup (one group of 4 rows per
-// wave) and, at K = 3072, one-wave workgroups, so more CUs share the few
-// hundred KB of weights and each wave's dot and epilogue chain is shorter
-// (GPT-2 Small batch-1 decode step 272 -> 252 us; 64 rows per 4-wave
-// workgroup before).
+// wave) and, at K = 3072 or N <= 1024, one-wave workgroups, so more CUs
+// share the few hundred KB of weights and each wave's dot and epilogue chain
+// is shorter (GPT-2 Small batch-1 decode step 272 -> 252 us; 64 rows per
+// 4-wave workgroup before; one-wave workgroups for the 768 x 768 attention
+// output projection: 247.5 -> 246.5 us).
 template <int EPI, int K, int SRC>
 void launch_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s) {
-    if (a.M <= 1) launch_fixed<1, EPI, K / 16, SRC, 1, (K == 3072 ? 1 : 4)>(a, s, f);
+    if (a.M <= 1 && (K == 3072 || a.N <= 1024)) launch_fixed<1, EPI, K / 16, SRC, 1, 1>(a, s, f);
+    else if (a.M <= 1) launch_fixed<1, EPI, K / 16, SRC, 1, 4>(a, s, f);
     else if (a.M <= 2) launch_fixed<2, EPI, K / 16, SRC>(a, s, f);
     else if (a.M <= 4) launch_fixed<4, EPI, K / 16, SRC>(a, s, f);
     else launch_mfma16<EPI, K / 64, SRC>(a, s, f);
