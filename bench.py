@@ -365,7 +365,8 @@ def bench_e2e(ie):
     """GPT-2 Small random-init N(0, 0.02), INT8 per-row
     linears (W8A8 as the reference engine), paged KV, prompt of 128 random ids,
     greedy decode of 256 tokens at batch 1 and 16.  tok/s counts decode steps
-    only (src/gpt2_engine.cu:754); MBU = bytes streamed per step x steps/s / 8 TB/s.
+    only (src/gpt2_engine.cu:754); MBU = bytes streamed per step (weights, LM head and the KV of
+    the timed steps' mean context) x steps/s / 8 TB/s.
     ttft_ms = prompt prefill + first token; also reported with the prompt fed
     through decode steps."""
     import numpy as np

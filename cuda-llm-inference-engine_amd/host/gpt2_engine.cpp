@@ -854,19 +854,23 @@ struct GPT2Engine::Impl {
         }
     }
 
-    double bytes_per_step(int B) const {
+    // Bytes one decode step streams for B sequences whose attention reads ctx
+    // cached tokens each.
+    double bytes_per_step(int B, double ctx) const {
         const double d = cfg.d_model, ff = cfg.d_ff, V = cfg.vocab_size;
         double w = cfg.n_layers * (3 * d * d + d * d + 2 * d * ff) * (fp32 ? 4.0 : 1.0);  // linear weights
         w += cfg.n_layers * 4.0 * (3 * d + d + ff + d) * (fp32 ? 1 : 2);   // biases (+ scales)
         w += cfg.n_layers * 4.0 * 4 * d;                                      // LayerNorm
         w += opt.int8_lm_head ? V * d + 4 * V : 4.0 * V * d;                  // LM head
-        const double kv = 2.0 * cfg.n_layers * (double)B * pos * d * (opt.kv_dtype == IE_KV_BF16 ? 2 : 4);
+        const double kv = 2.0 * cfg.n_layers * (double)B * ctx * d * (opt.kv_dtype == IE_KV_BF16 ? 2 : 4);
         return w + kv;
     }
 
     // tps counts the tokens the decode steps produced for sequences still
     // running (a sequence past its EOS is carried by the batch step but emits
-    // nothing); mbu counts the bytes every step streams.
+    // nothing); mbu counts the bytes the timed steps streamed: the n steps
+    // that ended at position pos read pos - n + 1 .. pos cached tokens, so
+    // their mean context is pos - (n - 1) / 2.
     void fill_tail_metrics(InferenceMetrics& m, const std::vector<float>& itl, float decode_ms, int B,
                            long decode_tokens) {
         const int n = (int)itl.size();
@@ -878,7 +882,7 @@ struct GPT2Engine::Impl {
             auto sorted = itl;
             std::sort(sorted.begin(), sorted.end());
             m.itl_p95_ms = n >= 20 ? sorted[(int)(n * 0.95)] : m.itl_max_ms;
-            m.mbu = (float)(bytes_per_step(B) * (1000.0 * n / decode_ms) / 8.0e12);
+            m.mbu = (float)(bytes_per_step(B, pos - (n - 1) / 2.0) * (1000.0 * n / decode_ms) / 8.0e12);
         }
         m.kv_cache_pct = 100.0f * ((pos + kBlock - 1) / kBlock) / nbps;
         size_t fr = 0, tot = 0;
@@ -914,7 +918,7 @@ void GPT2Engine::reset_session() { impl_->reset(); }
 int GPT2Engine::session_tokens() const { return impl_->pos; }
 const GPT2Config& GPT2Engine::config() const { return impl_->cfg; }
 const float* GPT2Engine::logits_device() const { return impl_->logits; }
-double GPT2Engine::step_bytes(int batch) const { return impl_->bytes_per_step(batch); }
+double GPT2Engine::step_bytes(int batch) const { return impl_->bytes_per_step(batch, impl_->pos + 1.0); }
 
 void GPT2Engine::prefill(const int* tokens, int batch, int len) {
     impl_->prefill(tokens, batch, len);

@@ -131,8 +131,9 @@ public:
      * (tokens on the host); logits of every sequence are left on the device. */
     void step(const int* tokens, int batch);
     const float* logits_device() const;
-    /* Bytes one decode step reads from HBM (weights, LM head, KV of the
-     * current context) for `batch` sequences; used for MBU. */
+    /* Bytes the next decode step reads from HBM (weights, LM head, and the
+     * KV of its pos + 1 cached tokens) for `batch` sequences.  The MBU of a
+     * generate call uses the mean context of its timed steps instead. */
     double step_bytes(int batch) const;
 
     /* Writes a random-initialised model in the reference's on-disk format,
