@@ -801,9 +801,9 @@ void launch_slice(const GemmArgs& a, hipStream_t s) {
     while (ks_log < 2 && (long long)groups * (2 << ks_log) <= 8LL * cus) ++ks_log;
     const unsigned blocks = ks_log == 0 ? (unsigned)std::min(groups, cus) : (unsigned)((groups << ks_log) + 7) / 8;
     // Plain loads: a wave instruction here reads 16 rows x 64 bytes, half of
-    // each 128-byte line, which non-temporal loads fetch once per half (M = 8
-    // / 16 at N = 8192: 0.58 / 0.556 -> 0.589 / 0.566 of HBM peak).  A ring of
-    // 2 sets of 8 loads: measured level with 4 sets.
+    // each 128-byte line, a pattern that streams slower with non-temporal
+    // loads (M = 8 / 16 at N = 8192: 0.58 / 0.556 -> 0.589 / 0.566 of HBM
+    // peak).  A ring of 2 sets of 8 loads: measured level with 4 sets.
     auto* k = a.M <= 8 ? gemv_i8_slice_kernel<EPI, false, 2, 8> : gemv_i8_slice_kernel<EPI, false, 2>;
     k<<<blocks, 512, 0, s>>>(a.M, a.N, ks_log, reinterpret_cast<const int8_t*>(a.A),
                              reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);

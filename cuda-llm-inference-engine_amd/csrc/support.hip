@@ -127,9 +127,9 @@ __global__ __launch_bounds__(256) void vocab_proj_kernel(int rows, const float* 
 //     4g .. +3; MFMA step (e, s) sums k = 64c + 16e + 4g + s over g for A
 //     and B alike, every k once.
 //   * Loads: read in that layout, a wave instruction would cover 16 rows x
-//     64 bytes, half of each 128-byte line, and non-temporal loads then
-//     fetch every line twice (a streaming lab over the 154 MB GPT-2 wte:
-//     5.3 TB/s against 6.6 TB/s for whole lines).  So instruction (rg, c)
+//     64 bytes, half of each 128-byte line, and with non-temporal loads that
+//     pattern streams slower (a lab over the 154 MB GPT-2 wte: 5.3 TB/s
+//     against 6.6 TB/s for 4 rows x 256 bytes per instruction).  So instruction (rg, c)
 //     reads rows 4rg .. 4rg + 3 x 256 contiguous bytes (lane l: row 4rg +
 //     l / 16, k = 64c + 4(l % 16)), and each wave passes its 12 fragments
 //     through its own 12 KB of LDS into the operand layout (XOR-swizzled
