@@ -73,20 +73,10 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* 
         const int which = lr / D;
         return which * d + h * D + (lr - which * D);
     };
-    const i32x4* w4 = reinterpret_cast<const i32x4*>(BT);
-    i32x4 wreg[G][CPL];
-    EpiIn ein[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) ein[g] = epi_load<IE_EPI_BIAS>(0, row_of(g), 3 * d, sB, bias, nullptr);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const i32x4* w = w4 + (size_t)row_of(g) * K16 + li;
-#pragma unroll
-        for (int t = 0; t < CPL; ++t) wreg[g][t] = w[16 * t];
-    }
-    // Wave 0's activation row and LayerNorm parameters are requested before
-    // the position / block-table lookups below: those are scalar loads in a
-    // dependent chain, and a wait for any scalar load waits for all of them.
+    // Wave 0's activation row and LayerNorm parameters are requested first:
+    // vector loads return in order, so behind the weights they would wait
+    // for them; and before the position / block-table lookups below, scalar
+    // loads in a dependent chain (a wait for any scalar load waits for all).
     float4 xv[kQaK / 256];
     LnVec<kQaK> lnp;
     if (wv == 0) {
@@ -109,6 +99,17 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* 
             stage_load<kQaK>(f.x + (size_t)b * d, xv, lane);
             ln_load<kQaK, kSrcLnQuant>(f, lnp, lane);
         }
+    }
+    const i32x4* w4 = reinterpret_cast<const i32x4*>(BT);
+    i32x4 wreg[G][CPL];
+    EpiIn ein[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) ein[g] = epi_load<IE_EPI_BIAS>(0, row_of(g), 3 * d, sB, bias, nullptr);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const i32x4* w = w4 + (size_t)row_of(g) * K16 + li;
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) wreg[g][t] = w[16 * t];
     }
     size_t slot[1];
     qkv_slots<1>(fb, 1, slot);
