@@ -239,22 +239,47 @@ __global__ __launch_bounds__(256, NCH >= 5 ? 1 : 2) void vocab_proj_mfma_kernel(
     };
     int t = blockIdx.x;
     if (t >= ntiles) return;  // uniform over the workgroup
-    // the first tile's weights are requested before the hidden rows are
-    // ready (they do not depend on them), so HEAD's LayerNorm hides behind them
+    // HEAD: this wave's hidden rows (w, w + 4, ...; rows <= 16) and the
+    // LayerNorm parameters are requested first, then the first tile's
+    // weights, which do not depend on them: loads return in order, so the
+    // rows arrive, and the LayerNorm runs, while the tile is in flight.
+    constexpr int NV = HEAD ? NCH : 1;  // float4s of a row per lane (d = 256 NCH)
+    float4 xr[HEAD ? 4 : 1][NV], gv[NV], bv[NV];
+    if constexpr (HEAD) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int r = w + 4 * rr;
+            if (r < rows) {
+                const float4* x4 = reinterpret_cast<const float4*>(h + (size_t)r * d);
+#pragma unroll
+                for (int j = 0; j < NV; ++j) xr[rr][j] = x4[lane + 64 * j];
+            }
+        }
+        const float4* g4 = reinterpret_cast<const float4*>(ha.gamma);
+        const float4* b4 = reinterpret_cast<const float4*>(ha.beta);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            gv[j] = g4[lane + 64 * j];
+            bv[j] = b4[lane + 64 * j];
+        }
+    }
     f32x4 wa[4][NCH], wb[4][NCH];
     load(wa, t);
     float4 hb[NCH][4];
     if constexpr (HEAD) {
         extern __shared__ float4 hs[];  // the normalised rows [rows][d / 4]
         const int d4 = d >> 2;
-        for (int r = w; r < rows; r += 4) {
-            const float4* x4 = reinterpret_cast<const float4*>(h + (size_t)r * d);
-            float s = 0.0f, s2 = 0.0f, mean, rs;
-            for (int j = lane; j < d4; j += 64) ln_accum(x4[j], s, s2);
-            ln_finish(s, s2, d, ha.eps, mean, rs);
-            const float4* g4 = reinterpret_cast<const float4*>(ha.gamma);
-            const float4* b4 = reinterpret_cast<const float4*>(ha.beta);
-            for (int j = lane; j < d4; j += 64) hs[r * d4 + j] = ln_apply(x4[j], g4[j], b4[j], mean, rs);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int r = w + 4 * rr;
+            if (r < rows) {
+                float s = 0.0f, s2 = 0.0f, mean, rs;
+#pragma unroll
+                for (int j = 0; j < NV; ++j) ln_accum(xr[rr][j], s, s2);
+                ln_finish(s, s2, d, ha.eps, mean, rs);
+#pragma unroll
+                for (int j = 0; j < NV; ++j) hs[r * d4 + lane + 64 * j] = ln_apply(xr[rr][j], gv[j], bv[j], mean, rs);
+            }
         }
         __syncthreads();
 #pragma unroll
