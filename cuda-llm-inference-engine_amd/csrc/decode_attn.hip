@@ -401,6 +401,173 @@ __device__ __forceinline__ void write_partial(float* __restrict__ dst, const flo
     }
 }
 
+// bf16 KV, d = 128: one wave's walk over chunks [tok0, tok1) of (sequence b,
+// kv head kvh) for its G query heads on bf16 MFMAs (block size 16, so a
+// 16-token chunk lies in one block).  The FMA form spends about 10 VALU
+// operations per KV element (unpack, 2 G FMAs) and measured VALU-bound at
+// bf16 (the chip issuing ~75% of its VALU rate); here:
+//   * QK: S^T (16 tokens x 16 columns: query heads 0 .. G - 1, the rest
+//     zero) = K_chunk (16 x 128) . Q^T on v_mfma_f32_16x16x32_bf16, K
+//     straight from the cache as the A operand (lane (t, g): token t, d =
+//     32 kb + 8 g .. + 8).  The scaled fp32 q is split exactly into three
+//     bf16 parts (top, middle and low 8 significant bits: hi + mid + lo = q),
+//     so every product is exact and only the fp32 sums round.  12 MFMAs.
+//   * Softmax in that output layout: lane (j, g) holds head j's scores of
+//     tokens 4 g .. 4 g + 3; a column's max and sum cross its four lanes
+//     with two swaps.
+//   * PV: O^T (128 x 16) += V^T . P^T on v_mfma_f32_16x16x16_bf16.  P^T is
+//     the score layout itself (lane (j, g): head j, tokens 4 g .. 4 g + 3),
+//     split into three bf16 parts as q; V^T comes from the chunk's V written
+//     row-major into the wave's LDS tile and read with ds_read_tr16_b64: lane
+//     16 g + 4 r + c supplies V[4 g + r][16 db + 4 c .. + 4], and the
+//     transpose hands lane 16 g + i the d-row 16 db + i of tokens 4 g ..
+//     4 g + 3 (the A operand).  24 MFMAs.
+// Chunks past tok1 re-read the last token (masked to -inf, weight 0).
+// Result: lane (j, g) holds m and l of head j and o[db][v] = O[head j][16 db
+// + 4 g + v] (unnormalised, base-2 domain, as the partials the merge reads).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+constexpr bool kMfAttn = true;
+constexpr int kMfTileRow = 144;  // LDS row of a V tile: 128 bf16 + 16 of padding (288 bytes)
+
+// x = hi + mid + lo exactly, each a bf16 bit pattern (truncation keeps the
+// top 8 significant bits; the remainders are exact in fp32).
+__device__ __forceinline__ void split3(float x, uint32_t& h, uint32_t& m, uint32_t& l) {
+    const uint32_t u = __float_as_uint(x);
+    const float r = x - __uint_as_float(u & 0xFFFF0000u);
+    const uint32_t ur = __float_as_uint(r);
+    const float lo = r - __uint_as_float(ur & 0xFFFF0000u);
+    h = u >> 16;
+    m = ur >> 16;
+    l = __float_as_uint(lo) >> 16;
+}
+
+template <int G>
+__device__ __forceinline__ void mfma_walk_bf16(const float* __restrict__ Q, const uint16_t* kcache,
+                                               const uint16_t* vcache, const int* __restrict__ bt, int b, int kvh,
+                                               int H_q, int H_kv, int tok0, int tok1, int lane, float qscale,
+                                               uint16_t* tile, float& m, float& l, f32x4_t (&o)[8]) {
+    constexpr int D = 128;
+    const int j = lane & 15, g = lane >> 4;
+    // q^T parts (B operand): lane (j, g) holds q_j[32 kb + 8 g .. + 8]
+    u32x4_t qp[3][4];
+    {
+        float qv[4][8];
+        if (j < G) {
+            const float4* q4 = reinterpret_cast<const float4*>(Q + ((size_t)b * H_q + (size_t)kvh * G + j) * D + 8 * g);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const float4 a = q4[8 * kb], c = q4[8 * kb + 1];
+                qv[kb][0] = a.x; qv[kb][1] = a.y; qv[kb][2] = a.z; qv[kb][3] = a.w;
+                qv[kb][4] = c.x; qv[kb][5] = c.y; qv[kb][6] = c.z; qv[kb][7] = c.w;
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qv[kb][e] = 0.0f;
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t h0, m0, l0, h1, m1, l1;
+                split3(qv[kb][2 * w] * qscale, h0, m0, l0);
+                split3(qv[kb][2 * w + 1] * qscale, h1, m1, l1);
+                qp[0][kb][w] = h0 | (h1 << 16);
+                qp[1][kb][w] = m0 | (m1 << 16);
+                qp[2][kb][w] = l0 | (l1 << 16);
+            }
+    }
+    m = -INFINITY;
+    l = 0.0f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) o[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (tok0 >= tok1) return;
+
+    const size_t tstride = (size_t)H_kv * D;
+    const uint16_t* kb0 = opaque_global(kcache) + (size_t)kvh * D + 8 * g;
+    const uint16_t* vb0 = opaque_global(vcache) + (size_t)kvh * D + 8 * g;
+    u32x4_t kf[2][4], vf[2][4];
+    int pn = bt[tok0 >> 4];
+    auto load = [&](u32x4_t (&kk)[4], u32x4_t (&vv)[4], int cs) {
+        const size_t row = (size_t)pn * 16 + (min(cs + j, tok1 - 1) & 15);
+        const u32x4_t* kp = reinterpret_cast<const u32x4_t*>(kb0 + row * tstride);
+        const u32x4_t* vp = reinterpret_cast<const u32x4_t*>(vb0 + row * tstride);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            kk[kb] = kp[4 * kb];
+            vv[kb] = vp[4 * kb];
+        }
+        pn = bt[min(cs + 16, tok1 - 1) >> 4];  // next chunk's block, one chunk ahead
+    };
+    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+    auto consume = [&](const u32x4_t (&kk)[4], const u32x4_t (&vv)[4], int cs) {
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int pt = 0; pt < 3; ++pt)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kk[kb]),
+                                                              __builtin_bit_cast(bf16x8_t, qp[pt][kb]), acc, 0, 0, 0);
+        // V rows into the tile (row j = token cs + j), read back transposed below
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) *reinterpret_cast<u32x4_t*>(tile + j * kMfTileRow + 32 * kb + 8 * g) = vv[kb];
+        float s[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s[v] = cs + 4 * g + v < tok1 ? acc[v] : -INFINITY;
+        float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        cm = max_xor32(max_xor16(cm));
+        const float mn = fmaxf(m, cm);
+        const float alpha = exp2f(m - mn);
+        float p[4], ps = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            p[v] = exp2f(s[v] - mn);
+            ps += p[v];
+        }
+        ps = sum_xor32(sum_xor16(ps));
+        l = fmaf(l, alpha, ps);
+        m = mn;
+        uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) split3(p[v], ph[v], pm[v], pl[v]);
+        i16x4_t pp[3];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            pp[0][v] = (short)ph[v];
+            pp[1][v] = (short)pm[v];
+            pp[2][v] = (short)pl[v];
+        }
+        const int r = (lane & 15) >> 2, c = lane & 3;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            o[db] *= alpha;
+            const i16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_i16x4*)((__attribute__((address_space(3))) uint16_t*)tile + (4 * g + r) * kMfTileRow + 16 * db + 4 * c));
+#pragma unroll
+            for (int pt = 0; pt < 3; ++pt) o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, pp[pt], o[db], 0, 0, 0);
+        }
+    };
+    int c0 = tok0;
+    load(kf[0], vf[0], c0);
+    bool more = true;
+    while (more) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (more) {
+                const bool nx = c0 + 16 < tok1;
+                if (nx) load(kf[u ^ 1], vf[u ^ 1], c0 + 16);
+                consume(kf[u], vf[u], c0);
+                c0 += 16;
+                more = nx;
+            }
+        }
+    }
+}
+
 // One-wave splits with a work-balanced partition (used when a launch has
 // many long splits).  With ragged context lengths a (b, split) grid leaves
 // many splits short or empty, so some CUs finish early while others still
@@ -419,7 +586,7 @@ __device__ __forceinline__ void write_partial(float* __restrict__ dst, const flo
 // lengths, so results do not depend on block placement.  Measured at ctx 8192
 // fp32 (four-head workgroups, one per CU): 0.676 of HBM peak against 0.599
 // for the (b, split) grid; bf16 at ctx 32768: 0.684 against 0.625.
-template <int D, int G, typename KV, bool BS16, int R, int NT, bool KL = false>
+template <int D, int G, typename KV, bool BS16, int R, int NT, bool KL = false, bool MF = false>
 __global__ __launch_bounds__(NT) void decode_attn_balanced_kernel(
     const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
     const int* __restrict__ block_table, const int* __restrict__ context_lens, int B, int H_q,
@@ -492,18 +659,42 @@ __global__ __launch_bounds__(NT) void decode_attn_balanced_kernel(
             const int seg = w - pre / q;
             const int tok0 = 16 * (max(lo, pre) - pre);
             const int tok1 = min(16 * (min(hi, post) - pre), lb);
-            float m[G], l[G], o[G][EPL];
-            if constexpr (KL)
-                split_partial_klds<G, NT / 64>(Q, kcache, vcache, block_table + (size_t)bj * nbps, bj, kvh, H_q, H_kv,
-                                                tok0, tok1, lane, qscale, m, l, o);
-            else
-                split_partial<D, G, KV, 1, BS16, R>(Q, kcache, vcache, block_table + (size_t)bj * nbps, bj, kvh, H_q,
-                                                 H_kv, block_size, tok0, tok1, 0, lane, qscale, m, l, o);
-            if (grp == 0 && seg < num_splits) {
+            if constexpr (MF) {
+                static_assert(D == 128 && sizeof(KV) == 2 && BS16, "bf16 MFMA walk: d = 128, block size 16");
+                __shared__ __attribute__((aligned(16))) uint16_t vtile[NT / 64][16 * kMfTileRow];
+                float mm, ll;
+                f32x4_t oo[8];
+                mfma_walk_bf16<G>(Q, reinterpret_cast<const uint16_t*>(kcache),
+                                  reinterpret_cast<const uint16_t*>(vcache), block_table + (size_t)bj * nbps, bj, kvh,
+                                  H_q, H_kv, tok0, tok1, lane, qscale, vtile[wid], mm, ll, oo);
+                const int hj = lane & 15, gq = lane >> 4;
+                if (hj < G && seg < num_splits) {
+                    float* dst = ws + (((size_t)bj * H_q + (size_t)kvh * G + hj) * num_splits + seg) * (D + 2);
 #pragma unroll
-                for (int g = 0; g < G; ++g)
-                    write_partial<D, G>(ws + (((size_t)bj * H_q + (size_t)kvh * G + g) * num_splits + seg) * (D + 2),
-                                        o[g], m[g], l[g], li);
+                    for (int db = 0; db < 8; ++db) {
+                        *reinterpret_cast<float2*>(dst + 16 * db + 4 * gq) = make_float2(oo[db][0], oo[db][1]);
+                        *reinterpret_cast<float2*>(dst + 16 * db + 4 * gq + 2) = make_float2(oo[db][2], oo[db][3]);
+                    }
+                    if (gq == 0) {
+                        dst[D] = mm;
+                        dst[D + 1] = ll;
+                    }
+                }
+            } else {
+                float m[G], l[G], o[G][EPL];
+                if constexpr (KL)
+                    split_partial_klds<G, NT / 64>(Q, kcache, vcache, block_table + (size_t)bj * nbps, bj, kvh, H_q,
+                                                    H_kv, tok0, tok1, lane, qscale, m, l, o);
+                else
+                    split_partial<D, G, KV, 1, BS16, R>(Q, kcache, vcache, block_table + (size_t)bj * nbps, bj, kvh,
+                                                     H_q, H_kv, block_size, tok0, tok1, 0, lane, qscale, m, l, o);
+                if (grp == 0 && seg < num_splits) {
+#pragma unroll
+                    for (int g = 0; g < G; ++g)
+                        write_partial<D, G>(
+                            ws + (((size_t)bj * H_q + (size_t)kvh * G + g) * num_splits + seg) * (D + 2), o[g], m[g],
+                            l[g], li);
+                }
             }
             if (post <= hi)  // the sequence ends here: its later slots are empty
                 for (int slot = seg + 1; slot < num_splits; ++slot) empty_slot(bj, slot);
@@ -579,9 +770,12 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
         // fp32 d = 128 with block size 16 lands K in LDS (G = 8 has no
         // register room for the ring beside its 8 heads' q and o).
         constexpr bool KL = D == 128 && sizeof(KV) == 4 && G <= 4;
-        auto* kb = (KL && a.block_size == 16) ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW, KL>
-                   : bs16                     ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW>
-                                              : decode_attn_balanced_kernel<D, G, KV, false, RW, NTW>;
+        // bf16 d = 128, G >= 4, block size 16: the MFMA walk
+        constexpr bool MF = D == 128 && sizeof(KV) == 2 && G >= 4 && kMfAttn;
+        auto* kb = (KL && a.block_size == 16)   ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW, KL>
+                   : (MF && a.block_size == 16) ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW, false, MF>
+                   : bs16                       ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW>
+                                                : decode_attn_balanced_kernel<D, G, KV, false, RW, NTW>;
         const int gy = a.H_kv / hw;
         const unsigned W = (unsigned)std::max(1, resident_per_cu((const void*)kb, 64 * hw) * num_cus() / gy);
         // chunks the plan covers (S x blocks per split, at least max_context_len)

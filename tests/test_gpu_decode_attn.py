@@ -279,11 +279,12 @@ def test_reference_sized_workspace(ie, orc):
 
 @pytest.mark.parametrize("bs", [16, 8])
 @pytest.mark.parametrize("kvdt", [0, 1])
-@pytest.mark.parametrize("d,G", [(64, 1), (128, 4)])
+@pytest.mark.parametrize("d,G", [(64, 1), (128, 4), (128, 8)])
 def test_balanced_partition_ragged_lengths(ie, orc, d, G, kvdt, bs):
     """Launches with many long one-wave splits cut the batch's chunks into
     equal workgroup ranges across sequence boundaries.  Ragged lengths from 0
-    to max, more than 64 sequences (two scan groups), 8 split slots."""
+    to max, more than 64 sequences (two scan groups), 8 split slots.  bf16,
+    d = 128, G >= 4 with block size 16 runs the bf16 MFMA walk."""
     r = rng(2000 + d + G + kvdt + bs)
     B, H_kv = 70, 2
     H_q = H_kv * G
