@@ -505,13 +505,18 @@ __device__ __forceinline__ void mfma_walk_bf16(const float* __restrict__ Q, cons
     };
     typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
     auto consume = [&](const u32x4_t (&kk)[4], const u32x4_t (&vv)[4], int cs) {
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        // four independent accumulators (one per 32-wide d block), added at the end
+        f32x4_t ac[4];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb) {
+            ac[kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int pt = 0; pt < 3; ++pt)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kk[kb]),
-                                                              __builtin_bit_cast(bf16x8_t, qp[pt][kb]), acc, 0, 0, 0);
+                ac[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kk[kb]),
+                                                                 __builtin_bit_cast(bf16x8_t, qp[pt][kb]), ac[kb], 0, 0,
+                                                                 0);
+        }
+        const f32x4_t acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
         // V rows into the tile (row j = token cs + j), read back transposed below
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) *reinterpret_cast<u32x4_t*>(tile + j * kMfTileRow + 32 * kb + 8 * g) = vv[kb];
