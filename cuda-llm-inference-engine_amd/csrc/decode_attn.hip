@@ -429,7 +429,6 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-constexpr bool kMfAttn = true;
 constexpr int kMfTileRow = 144;  // LDS row of a V tile: 128 bf16 + 16 of padding (288 bytes)
 
 // x = hi + mid + lo exactly, each a bf16 bit pattern (truncation keeps the
@@ -666,9 +665,9 @@ __global__ __launch_bounds__(NT) void decode_attn_balanced_kernel(
             const int tok1 = min(16 * (min(hi, post) - pre), lb);
             if constexpr (MF) {
                 static_assert(D == 128 && sizeof(KV) == 2 && BS16, "bf16 MFMA walk: d = 128, block size 16");
-                __shared__ __attribute__((aligned(16))) uint16_t vtile[NT / 64][16 * kMfTileRow];
                 float mm, ll;
                 f32x4_t oo[8];
+                __shared__ __attribute__((aligned(16))) uint16_t vtile[NT / 64][16 * kMfTileRow];
                 mfma_walk_bf16<G>(Q, reinterpret_cast<const uint16_t*>(kcache),
                                   reinterpret_cast<const uint16_t*>(vcache), block_table + (size_t)bj * nbps, bj, kvh,
                                   H_q, H_kv, tok0, tok1, lane, qscale, vtile[wid], mm, ll, oo);
@@ -775,8 +774,10 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
         // fp32 d = 128 with block size 16 lands K in LDS (G = 8 has no
         // register room for the ring beside its 8 heads' q and o).
         constexpr bool KL = D == 128 && sizeof(KV) == 4 && G <= 4;
-        // bf16 d = 128, G >= 4, block size 16: the MFMA walk
-        constexpr bool MF = D == 128 && sizeof(KV) == 2 && G >= 4 && kMfAttn;
+        // bf16 d = 128, G >= 4, block size 16: the MFMA walk (an fp32 form on
+        // v_mfma_f32_16x16x4_f32 measured 0.35 against 0.61 of HBM peak at
+        // G = 8, so fp32 keeps the FMA walk)
+        constexpr bool MF = D == 128 && sizeof(KV) == 2 && G >= 4;
         auto* kb = (KL && a.block_size == 16)   ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW, KL>
                    : (MF && a.block_size == 16) ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW, false, MF>
                    : bs16                       ? decode_attn_balanced_kernel<D, G, KV, true, RW, NTW>
