@@ -21,13 +21,17 @@ struct Slice {
     uint32_t w[WORDS];
 };
 
-template <int EPL, typename KV>
+// NTL: non-temporal loads (for a cache stream larger than the caches keep).
+template <int EPL, typename KV, bool NTL = false>
 __device__ __forceinline__ void load_raw(const KV* __restrict__ p, Slice<EPL, KV>& s) {
     constexpr int W = Slice<EPL, KV>::WORDS;
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
     if constexpr (W % 4 == 0) {
 #pragma unroll
         for (int i = 0; i < W / 4; ++i) {
-            const uint4 v = reinterpret_cast<const uint4*>(p)[i];
+            const u32x4v* a = reinterpret_cast<const u32x4v*>(p) + i;
+            const u32x4v v = NTL ? __builtin_nontemporal_load(a) : *a;
             s.w[4 * i + 0] = v.x;
             s.w[4 * i + 1] = v.y;
             s.w[4 * i + 2] = v.z;
@@ -35,7 +39,8 @@ __device__ __forceinline__ void load_raw(const KV* __restrict__ p, Slice<EPL, KV
         }
     } else {
         static_assert(W == 2, "slice width");
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        const u32x2v* a = reinterpret_cast<const u32x2v*>(p);
+        const u32x2v v = NTL ? __builtin_nontemporal_load(a) : *a;
         s.w[0] = v.x;
         s.w[1] = v.y;
     }
@@ -72,7 +77,7 @@ struct Chunk {
 };
 
 // Loads this lane's slices of tokens c0 + 4j + grp (j < T) of a chunk.
-template <int D, typename KV, int T>
+template <int D, typename KV, int T, bool NTL = false>
 __device__ __forceinline__ void load_chunk(Chunk<D, KV, T>& c, int c0, int grp, int tok1,
                                            const int* __restrict__ bt, int block_size,
                                            size_t tok_stride, const KV* kbase, const KV* vbase) {
@@ -86,14 +91,14 @@ __device__ __forceinline__ void load_chunk(Chunk<D, KV, T>& c, int c0, int grp, 
         const int pc = min(pos, tok1 - 1);
         const int blk = pc / block_size;
         const size_t row = (size_t)bt[blk] * block_size + (pc - blk * block_size);
-        load_raw(kbase + row * tok_stride, c.k[j]);
-        load_raw(vbase + row * tok_stride, c.v[j]);
+        load_raw<D / 16, KV, NTL>(kbase + row * tok_stride, c.k[j]);
+        load_raw<D / 16, KV, NTL>(vbase + row * tok_stride, c.v[j]);
     }
 }
 
 // Block size 16: the chunk's tokens (c0 a multiple of 4T) lie in blocks
 // phys[0], phys[1], ... (16 tokens each), the same for every lane.
-template <int D, typename KV, int T>
+template <int D, typename KV, int T, bool NTL = false>
 __device__ __forceinline__ void load_chunk16(Chunk<D, KV, T>& c, int c0, int grp, int tok1,
                                              const int (&phys)[(T + 3) / 4], size_t tok_stride,
                                              const KV* kbase, const KV* vbase) {
@@ -103,8 +108,8 @@ __device__ __forceinline__ void load_chunk16(Chunk<D, KV, T>& c, int c0, int grp
         c.valid[j] = pos < tok1;
         const int pc = min(pos, tok1 - 1);
         const size_t row = (size_t)phys[j / 4] * 16 + (pc & 15);
-        load_raw(kbase + row * tok_stride, c.k[j]);
-        load_raw(vbase + row * tok_stride, c.v[j]);
+        load_raw<D / 16, KV, NTL>(kbase + row * tok_stride, c.k[j]);
+        load_raw<D / 16, KV, NTL>(vbase + row * tok_stride, c.v[j]);
     }
 }
 
@@ -164,7 +169,7 @@ __device__ __forceinline__ void consume_chunk(const Chunk<D, KV, T>& c, const fl
 // patch that substitutes the token it has just appended (held in LDS) for
 // that token's cache row, which the early loads may have read before it was
 // written.  The arithmetic and its order are the same either way.
-template <int D, int G, typename KV, int WPS, bool BS16, int R>
+template <int D, int G, typename KV, int WPS, bool BS16, int R, bool NTL = false>
 struct SplitWalk {
     static constexpr int EPL = D / 16;
     // Chunk rows and ring depth: R chunks of 4T tokens cycle through the
@@ -201,10 +206,10 @@ struct SplitWalk {
     }
     __device__ __forceinline__ void next(Chunk<D, KV, T>& c, int cs) {
         if constexpr (BS16) {
-            load_chunk16(c, cs, grp, tok1, pn, tok_stride, kbase, vbase);
+            load_chunk16<D, KV, T, NTL>(c, cs, grp, tok1, pn, tok_stride, kbase, vbase);
             prefetch(cs + STEP);
         } else {
-            load_chunk(c, cs, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
+            load_chunk<D, KV, T, NTL>(c, cs, grp, tok1, bt, block_size, tok_stride, kbase, vbase);
         }
     }
 
@@ -276,7 +281,7 @@ struct SplitWalk {
     }
 };
 
-template <int D, int G, typename KV, int WPS, bool BS16, int R>
+template <int D, int G, typename KV, int WPS, bool BS16, int R, bool NTL = false>
 __device__ __forceinline__ void split_partial(const float* __restrict__ Q, const KV* __restrict__ kcache,
                                               const KV* __restrict__ vcache, const int* __restrict__ bt,
                                               int b, int kvh, int H_q, int H_kv, int block_size, int tok0,
@@ -284,7 +289,7 @@ __device__ __forceinline__ void split_partial(const float* __restrict__ Q, const
                                               float (&l)[G], float (&o)[G][D / 16], int pn0 = -1) {
     constexpr int EPL = D / 16;
     const int li = lane & 15;
-    SplitWalk<D, G, KV, WPS, BS16, R> w;
+    SplitWalk<D, G, KV, WPS, BS16, R, NTL> w;
     w.begin(kcache, vcache, bt, kvh, H_kv, block_size, tok0, tok1, wave, lane, pn0);
     float q[G][EPL];
 #pragma unroll

@@ -316,7 +316,7 @@ done:
 
 // With WPS == 1 a workgroup holds blockDim.x / 64 waves, one per KV head
 // (kv head = blockIdx.y * waves + wave), all on the same split.
-template <int D, int G, typename KV, int WPS, bool BS16, int R, int NT>
+template <int D, int G, typename KV, int WPS, bool BS16, int R, int NT, bool NTL = false>
 __global__ __launch_bounds__(NT) void decode_attn_split_kernel(
     const float* __restrict__ Q, const KV* __restrict__ kcache, const KV* __restrict__ vcache,
     const int* __restrict__ block_table, const int* __restrict__ context_lens, int H_q,
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(NT) void decode_attn_split_kernel(
     const int tok1 = (int)min(t0l + span, lim);
 
     float m[G], l[G], o[G][EPL];
-    split_partial<D, G, KV, WPS, BS16, R>(Q, kcache, vcache, bt, b, kvh, H_q, H_kv, block_size, tok0, tok1,
+    split_partial<D, G, KV, WPS, BS16, R, NTL>(Q, kcache, vcache, bt, b, kvh, H_q, H_kv, block_size, tok0, tok1,
                                        wave, lane, qscale, m, l, o, pn0);
     // The partial of this split; an empty split writes o = 0, m = -inf, l = 0.
     // With a single split the partial is the result: O = o / l, written
@@ -750,6 +750,15 @@ int resident_per_cu(const void* f, int threads) {
     return n;
 }
 
+// Bytes of K and V a launch may read (every sequence at the plan's longest
+// context), and the size past which the cache is streamed non-temporally.
+long long kv_stream_bytes(const DecodeArgs& a) {
+    const long long ctx = std::min<long long>((long long)a.num_splits * a.blocks_per_split * a.block_size,
+                                              (long long)a.num_blocks_per_seq * a.block_size);
+    return (long long)a.B * ctx * a.H_kv * a.d * 2 * (a.kv_dtype == IE_KV_BF16 ? 2 : 4);
+}
+constexpr long long kStreamKvBytes = 32ll << 20;
+
 template <int D, int G, typename KV>
 void launch_split(const DecodeArgs& a, hipStream_t s) {
     const float qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
@@ -807,15 +816,24 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
     constexpr int WF = 8;
     constexpr bool WF_FITS = G <= 4;
     const bool few = WF_FITS && !wave && (long long)a.num_splits * a.H_kv <= kFewUnits;
+    // Multi-wave splits stream the cache with non-temporal loads when the
+    // launch reads more of it than the caches would keep (kv_stream_bytes):
+    // cfg3 (50 MB) 15.3 -> 13.9 us; one-wave splits measured slightly slower
+    // with them and keep plain loads.
+    const bool ntl = kv_stream_bytes(a) > kStreamKvBytes;
     using KernelT = decltype(&decode_attn_split_kernel<D, G, KV, 4, true, 2, 256>);
     KernelT k = wave ? (bs16 ? decode_attn_split_kernel<D, G, KV, 1, true, RW, NTW>
                              : decode_attn_split_kernel<D, G, KV, 1, false, RW, NTW>)
-                     : (bs16 ? decode_attn_split_kernel<D, G, KV, 4, true, 2, 256>
-                             : decode_attn_split_kernel<D, G, KV, 4, false, 2, 256>);
+                : ntl ? (bs16 ? decode_attn_split_kernel<D, G, KV, 4, true, 2, 256, true>
+                              : decode_attn_split_kernel<D, G, KV, 4, false, 2, 256, true>)
+                      : (bs16 ? decode_attn_split_kernel<D, G, KV, 4, true, 2, 256>
+                              : decode_attn_split_kernel<D, G, KV, 4, false, 2, 256>);
     if constexpr (WF_FITS)
         if (few)
-            k = bs16 ? decode_attn_split_kernel<D, G, KV, WF, true, 2, 64 * WF>
-                     : decode_attn_split_kernel<D, G, KV, WF, false, 2, 64 * WF>;
+            k = ntl ? (bs16 ? decode_attn_split_kernel<D, G, KV, WF, true, 2, 64 * WF, true>
+                            : decode_attn_split_kernel<D, G, KV, WF, false, 2, 64 * WF, true>)
+                    : (bs16 ? decode_attn_split_kernel<D, G, KV, WF, true, 2, 64 * WF>
+                            : decode_attn_split_kernel<D, G, KV, WF, false, 2, 64 * WF>);
     k<<<grid, wave ? 64 * hw : few ? 64 * WF : 256, 0, s>>>(
         a.Q, static_cast<const KV*>(a.k_cache), static_cast<const KV*>(a.v_cache),
         a.block_table, a.context_lens, a.H_q, a.H_kv, a.block_size, a.num_blocks_per_seq,

@@ -66,6 +66,9 @@ struct GemvFusion {
     const int* ids = nullptr;
     const float* wte = nullptr;
     const float* wpe = nullptr;
+    // launch_qkv_attn only: read the cache with non-temporal loads (a step's
+    // cache stream larger than the caches keep beside the weights)
+    bool kv_stream = false;
 };
 // The engine's QKV projection + decode attention in one launch, one
 // workgroup per (sequence, head) (qkv_attn.hip): f as for the kEpiQKV GEMV

@@ -40,7 +40,8 @@ constexpr int kQaK = 768;    // d_model (the projection's K)
 // EMB: the first layer's launch builds x[b] itself (f.ids set): the
 // embedding wte[ids[b]] + wpe[positions[b]], which head 0's workgroup also
 // stores to x for the layer's residual adds; the embedding launch is saved.
-template <int D, typename KV, bool EMB>
+// NTL: the cache walk reads with non-temporal loads (f.kv_stream).
+template <int D, typename KV, bool EMB, bool NTL>
 __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* __restrict__ BT,
                                                                  const float* __restrict__ sB,
                                                                  const float* __restrict__ bias, GemvFusion f,
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_kernel(const int32_t* 
     // Tokens 0 .. pos of the sequence (never past its block-table row).
     const int pos = f.positions[b];
     const int tok1 = (int)min((long long)pos + 1, (long long)f.nbps * f.block_size);
-    SplitWalk<D, 1, KV, kQaWaves, true, 2> walk;
+    SplitWalk<D, 1, KV, kQaWaves, true, 2, NTL> walk;
     walk.begin(kcache, vcache, fb.table, h, H, f.block_size, 0, tok1, wv, lane);
 
     if (wv == 0) stage_compute<kQaK, kSrcLnQuant>(xv, f, lnp, reinterpret_cast<int32_t*>(a_lds), &s_sa[0], lane);
@@ -184,20 +185,26 @@ void launch_qkv_attn(int B, int H, const int32_t* BT, const float* sB, const flo
     constexpr int D = 64;
     const float qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
     const dim3 grid(H, B);
-    auto go = [&](auto emb) {
-        constexpr bool E = decltype(emb)::value;
+    auto go = [&](auto emb, auto ntl) {
+        constexpr bool E = decltype(emb)::value, N = decltype(ntl)::value;
         if (f.kv_dtype == IE_KV_BF16)
-            qkv_attn_kernel<D, uint16_t, E><<<grid, 64 * kQaWaves, 0, s>>>(
+            qkv_attn_kernel<D, uint16_t, E, N><<<grid, 64 * kQaWaves, 0, s>>>(
                 BT, sB, bias, f, static_cast<const uint16_t*>(f.kc), static_cast<const uint16_t*>(f.vc), H, qscale,
                 O);
         else
-            qkv_attn_kernel<D, float, E><<<grid, 64 * kQaWaves, 0, s>>>(
+            qkv_attn_kernel<D, float, E, N><<<grid, 64 * kQaWaves, 0, s>>>(
                 BT, sB, bias, f, static_cast<const float*>(f.kc), static_cast<const float*>(f.vc), H, qscale, O);
     };
+    auto go_n = [&](auto emb) {
+        if (f.kv_stream)
+            go(emb, std::true_type{});
+        else
+            go(emb, std::false_type{});
+    };
     if (f.ids)
-        go(std::true_type{});
+        go_n(std::true_type{});
     else
-        go(std::false_type{});
+        go_n(std::false_type{});
 }
 
 }  // namespace ie
