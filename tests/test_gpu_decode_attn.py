@@ -315,3 +315,33 @@ def test_balanced_partition_two_slots_and_invariance(ie, orc):
     b = run_gpu(ie, Q, kc2, vc2, table2, lens, 1024, 16, H_kv, splits=2)
     assert rel_err(a, want) < REL
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("kvdt", [0, 1])
+@pytest.mark.parametrize("H_kv,d,G", [(4, 128, 1), (12, 64, 1), (4, 128, 4)])
+def test_streamed_cache_loads_same_bits(ie, orc, H_kv, d, G, kvdt):
+    """Launches whose cache reads (batch x plan context x heads x d x 2 x
+    element size) pass 32 MiB load the cache with non-temporal loads in the
+    multi-wave split layouts: eight waves per split at <= 64 (kv head, split)
+    units per sequence (H_kv 4, 16 splits), four above (H_kv 12).  32
+    sequences of 1024 tokens pass the threshold, one alone does not; the
+    cache policy changes no arithmetic, so each sequence gets the same bits
+    either way."""
+    r = rng(3000 + H_kv + d + G + kvdt)
+    B, ctx = 32, 1024
+    H_q = H_kv * G
+    lens = np.full(B, ctx)
+    lens[7] = 999
+    kc, vc, table, _, _ = make_paged_cache(r, B, H_kv, d, lens, 16)
+    Q = r.standard_normal((B, H_q, d)).astype(np.float32)
+    if kvdt:
+        kc, vc = bf16_bits(kc), bf16_bits(vc)
+    esz = 2 if kvdt else 4
+    assert B * ctx * H_kv * d * 2 * esz > 32 << 20 > ctx * H_kv * d * 2 * esz
+    want = orc.decode_attn(Q, kc, vc, table, lens, ctx, 16, H_kv, kv_dtype=kvdt)
+    got = run_gpu(ie, Q, kc, vc, table, lens, ctx, 16, H_kv, kv_dtype=kvdt, splits=16)
+    assert rel_err(got, want) < REL
+    for b in (0, 7, 31):
+        one = run_gpu(ie, Q[b:b + 1], kc, vc, table[b:b + 1], lens[b:b + 1], ctx, 16, H_kv, kv_dtype=kvdt,
+                      splits=16)
+        assert np.array_equal(one[0], got[b]), b
