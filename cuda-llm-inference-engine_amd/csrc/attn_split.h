@@ -133,11 +133,11 @@ __device__ __forceinline__ void consume_chunk(const Chunk<D, KV, T>& c, const fl
         for (int j = 1; j < T; ++j) cm = fmaxf(cm, s[j]);
         cm = max_xor32(max_xor16(cm));
         const float mn = fmaxf(m[g], cm);
-        const float alpha = exp2f(m[g] - mn);
+        const float alpha = exp2_sm(m[g] - mn);
         float p[T], psum = 0.0f;
 #pragma unroll
         for (int j = 0; j < T; ++j) {
-            p[j] = exp2f(s[j] - mn);
+            p[j] = exp2_sm(s[j] - mn);
             psum += p[j];
         }
         l[g] = fmaf(l[g], alpha, psum);
@@ -337,7 +337,7 @@ __device__ __forceinline__ void split_finish_lds(int b, int kvh, int H_q, int sp
         if (mx != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < WPS; ++w) {
-                const float f = exp2f(sm_m[w][g] - mx);
+                const float f = exp2_sm(sm_m[w][g] - mx);
                 ov = fmaf(sm_o[w][g][dd], f, ov);
                 lv = fmaf(sm_l[w][g], f, lv);
             }

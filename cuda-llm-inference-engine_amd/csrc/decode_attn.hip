@@ -102,7 +102,7 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ w, int S,
             const float* p = w + (size_t)s * (D + 2);
             const float ls = p[D + 1];
             on = ls > 0.0f;
-            f = on ? exp2f(p[D] - mx) : 0.0f;
+            f = on ? exp2_sm(p[D] - mx) : 0.0f;
             l = fmaf(ls, f, l);
         }
         // Splits with l > 0; an empty one (l = 0, whose o the balanced pass
@@ -272,11 +272,11 @@ __device__ __forceinline__ void split_partial_klds(const float* __restrict__ Q, 
             float cm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
             cm = max_xor32(max_xor16(cm));
             const float mn = fmaxf(m[g], cm);
-            const float alpha = exp2f(m[g] - mn);
+            const float alpha = exp2_sm(m[g] - mn);
             float p[T], psum = 0.0f;
 #pragma unroll
             for (int j = 0; j < T; ++j) {
-                p[j] = exp2f(sc[j] - mn);
+                p[j] = exp2_sm(sc[j] - mn);
                 psum += p[j];
             }
             l[g] = fmaf(l[g], alpha, psum);
@@ -531,11 +531,11 @@ __device__ __forceinline__ void mfma_walk_bf16(const float* __restrict__ Q, cons
         float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
         cm = max_xor32(max_xor16(cm));
         const float mn = fmaxf(m, cm);
-        const float alpha = exp2f(m - mn);
+        const float alpha = exp2_sm(m - mn);
         float p[4], ps = 0.0f;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            p[v] = exp2f(s[v] - mn);
+            p[v] = exp2_sm(s[v] - mn);
             ps += p[v];
         }
         ps = sum_xor32(sum_xor16(ps));

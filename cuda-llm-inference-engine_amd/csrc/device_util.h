@@ -176,4 +176,11 @@ __device__ __forceinline__ const T* opaque_global(const T* p) {
     return (const T*)g;
 }
 
+// 2^x as the one instruction v_exp_f32.  exp2f wraps it in a range step
+// (compare, select, add, select, ldexp) so that results below 2^-126 come out
+// denormal instead of flushed; every other result is the same bits.  The
+// softmax weights are 2^(s - running max) <= 1, and a weight below 2^-126 is
+// added to sums that already hold the running maximum's weight of 1.
+__device__ __forceinline__ float exp2_sm(float x) { return __builtin_amdgcn_exp2f(x); }
+
 }  // namespace ie

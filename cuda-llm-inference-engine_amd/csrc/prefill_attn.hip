@@ -143,11 +143,11 @@ __device__ __forceinline__ void consume(const Chunk<D, KV>& c, int c0, int g, co
     cm = max_xor32(max_xor16(cm));
     const float mn = fmaxf(m, cm);
     const float mu = mn == -INFINITY ? 0.0f : mn;  // no key yet: keep o, l at 0
-    const float alpha = exp2f(m - mu);
+    const float alpha = exp2_sm(m - mu);
     float p[4], ls = 0.0f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        p[v] = exp2f(s[v] - mu);
+        p[v] = exp2_sm(s[v] - mu);
         ls += p[v];
     }
     ls = sum_xor32(sum_xor16(ls));
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(
     float f[kWaves], L = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-        f[w] = sm_m[w][qq] == -INFINITY ? 0.0f : exp2f(sm_m[w][qq] - mx);
+        f[w] = sm_m[w][qq] == -INFINITY ? 0.0f : exp2_sm(sm_m[w][qq] - mx);
         L = fmaf(f[w], sm_l[w][qq], L);
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
