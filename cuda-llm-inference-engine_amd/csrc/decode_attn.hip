@@ -782,7 +782,7 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
     // Scalar block ids measured 12% faster for bf16 KV at ctx 8192 and 1%
     // slower for fp32 one-wave splits (where the per-lane table loads already
     // sit behind the chunk's own KV loads); fp32 long splits keep those.
-    const bool bs16 = a.block_size == 16 && !(wave && sizeof(KV) == 4);
+    const bool bs16 = a.block_size == 16 && !(wave && sizeof(KV) == 4 && G < 8);
     if (wave && a.num_splits >= 2 && a.B <= kBalancedMaxB) {
         // As many workgroups as are resident at once (occupancy x CUs), so the
         // equal ranges all run in one round.
