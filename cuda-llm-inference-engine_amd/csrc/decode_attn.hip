@@ -781,7 +781,9 @@ void launch_split(const DecodeArgs& a, hipStream_t s) {
     const dim3 grid(a.num_splits, a.H_kv / hw, a.B);
     // Scalar block ids measured 12% faster for bf16 KV at ctx 8192 and 1%
     // slower for fp32 one-wave splits (where the per-lane table loads already
-    // sit behind the chunk's own KV loads); fp32 long splits keep those.
+    // sit behind the chunk's own KV loads); fp32 long splits keep those,
+    // except at G = 8, whose walk is VALU-bound and gains 5% without the
+    // per-lane table loads and block arithmetic.
     const bool bs16 = a.block_size == 16 && !(wave && sizeof(KV) == 4 && G < 8);
     if (wave && a.num_splits >= 2 && a.B <= kBalancedMaxB) {
         // As many workgroups as are resident at once (occupancy x CUs), so the
