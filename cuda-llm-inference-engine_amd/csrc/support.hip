@@ -117,7 +117,9 @@ __global__ __launch_bounds__(256) void vocab_proj_kernel(int rows, const float* 
 // when d = 256 * NCH (GPT-2: NCH = 3): a 16-vocabulary-row tile of logits^T =
 // wte tile (A) x hidden^T (B, zero past `rows`).
 //   * Persistent workgroups walk the tiles (tile = blockIdx.x + n * gridDim.x)
-//     with the next tile's weights loaded while the current one is computed.
+//     with the next tile's weights loaded while the current one is computed
+//     (the fused head, one workgroup per CU with its 512 registers per lane:
+//     the next two tiles; batch-1 / 16 decode step -1.0 / -0.9 us, same bits).
 //   * The four waves split K: wave w owns k in [w d/4, (w+1) d/4), NCH chunks
 //     of 64.  It holds its quarter of the hidden rows in registers for the
 //     whole kernel, so nothing is staged per tile, and its partial 16 x 16
@@ -189,7 +191,7 @@ __device__ __forceinline__ void finalize_row(int B, int b, unsigned long long* k
 }
 
 template <int NCH, bool HEAD = false>
-__global__ __launch_bounds__(256, NCH >= 5 ? 1 : 2) void vocab_proj_mfma_kernel(int rows, const float* __restrict__ h,
+__global__ __launch_bounds__(256, NCH >= 5 || HEAD ? 1 : 2) void vocab_proj_mfma_kernel(int rows, const float* __restrict__ h,
                                                                  const float* __restrict__ wte,
                                                                  float* __restrict__ logits, int d, int V,
                                                                  HeadArgs ha) {
@@ -263,8 +265,9 @@ __global__ __launch_bounds__(256, NCH >= 5 ? 1 : 2) void vocab_proj_mfma_kernel(
             bv[j] = b4[lane + 64 * j];
         }
     }
-    f32x4 wa[4][NCH], wb[4][NCH];
+    f32x4 wa[4][NCH], wb[4][NCH], wc[4][NCH];
     load(wa, t);
+    if constexpr (HEAD) load(wb, t + gridDim.x);
     float4 hb[NCH][4];
     if constexpr (HEAD) {
         extern __shared__ float4 hs[];  // the normalised rows [rows][d / 4]
@@ -339,15 +342,34 @@ __global__ __launch_bounds__(256, NCH >= 5 ? 1 : 2) void vocab_proj_mfma_kernel(
         }
         par ^= 1;
     };
-    while (true) {
-        load(wb, t + gridDim.x);
-        tile(wa, t);
-        t += gridDim.x;
-        if (t >= ntiles) break;
-        load(wa, t + gridDim.x);
-        tile(wb, t);
-        t += gridDim.x;
-        if (t >= ntiles) break;
+    if constexpr (HEAD) {
+        // three tiles in the ring: two in flight while one is computed
+        const int G3 = 2 * (int)gridDim.x;
+        while (true) {
+            load(wc, t + G3);
+            tile(wa, t);
+            t += gridDim.x;
+            if (t >= ntiles) break;
+            load(wa, t + G3);
+            tile(wb, t);
+            t += gridDim.x;
+            if (t >= ntiles) break;
+            load(wb, t + G3);
+            tile(wc, t);
+            t += gridDim.x;
+            if (t >= ntiles) break;
+        }
+    } else {
+        while (true) {
+            load(wb, t + gridDim.x);
+            tile(wa, t);
+            t += gridDim.x;
+            if (t >= ntiles) break;
+            load(wa, t + gridDim.x);
+            tile(wb, t);
+            t += gridDim.x;
+            if (t >= ntiles) break;
+        }
     }
     if constexpr (HEAD) {
         if (w == 0) {
