@@ -197,7 +197,7 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(
 // C[4 * (l / 16) + v][n0 + l % 16].  The activation block is staged in LDS
 // (or built there by the fused prologue); weight loads run U steps ahead of
 // the MFMAs.
-template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false, int NWV = 4, int RS = 16>
+template <int EPI, int K64, int SRC = kSrcInt8, bool NT = false, int NWV = 4, int RS = 16, int FW = 16>
 __global__ __launch_bounds__(64 * NWV) void gemv_i8_mfma16_kernel(
     int M, int N, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
@@ -227,7 +227,11 @@ __global__ __launch_bounds__(64 * NWV) void gemv_i8_mfma16_kernel(
     __shared__ i32x4 red[NWV - 1][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, kq = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    // FW < 16 features per workgroup (so a small N still covers every CU):
+    // columns FW .. 15 re-read feature FW - 1 (the same lines, fetched once)
+    // and are not stored.
+    static_assert(FW == 16 || (FW < 16 && EPI != kEpiQKV), "QKV rows keep 16 features");
+    const int n0 = blockIdx.x * FW;
     const int kb = wave * KW;  // first K step of this wave
 
     auto ldw = [&](const int8_t* p) {
@@ -246,7 +250,7 @@ __global__ __launch_bounds__(64 * NWV) void gemv_i8_mfma16_kernel(
             ein[v] = epi_load<EPI>(min(4 * kq + v, M - 1), min(n0 + col, N - 1), N, sB, bias, residual);
         if constexpr (EPI == kEpiQKV) qkv_slots<16>(f, M, slot);
     }
-    const int8_t* w = BT + (size_t)min(n0 + col, N - 1) * K + kq * 16;
+    const int8_t* w = BT + (size_t)min(n0 + min(col, FW - 1), N - 1) * K + kq * 16;
     i32x4 wv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) wv[u] = ldw(w + (size_t)(kb + u) * 64);
@@ -315,7 +319,7 @@ __global__ __launch_bounds__(64 * NWV) void gemv_i8_mfma16_kernel(
 #pragma unroll
     for (int w = 0; w < NWV - 1; ++w) acc += red[w][lane];
     const int n = n0 + col;
-    if (n < N) {
+    if (n < N && col < FW) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int m = 4 * kq + v;
@@ -777,17 +781,24 @@ void launch_mfma16(const GemmArgs& a, hipStream_t s, const GemvFusion& f = GemvF
     // a CU keeps only so many bytes in flight (GPT-2 batch-16 decode step
     // 413.7 -> 368.7 us, same bits; 1, 2 and 8 rows measured slower).  QKV
     // epilogue rows carry cache slots and keep 16.
-    auto go = [&](auto rsc) {
-        constexpr int RS = decltype(rsc)::value;
-        auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true, NWV, RS>
-                     : gemv_i8_mfma16_kernel<EPI, K64, SRC, false, NWV, RS>;
-        k<<<dim3(blocks, (unsigned)((a.M + RS - 1) / RS)), 64 * NWV, 0, s>>>(
+    auto go = [&](auto rsc, auto fwc) {
+        constexpr int RS = decltype(rsc)::value, FW = decltype(fwc)::value;
+        auto* k = nt ? gemv_i8_mfma16_kernel<EPI, K64, SRC, true, NWV, RS, FW>
+                     : gemv_i8_mfma16_kernel<EPI, K64, SRC, false, NWV, RS, FW>;
+        k<<<dim3((unsigned)((a.N + FW - 1) / FW), (unsigned)((a.M + RS - 1) / RS)), 64 * NWV, 0, s>>>(
             a.M, a.N, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB,
             a.bias, a.residual, a.C, f);
     };
     if constexpr (EPI != kEpiQKV)
-        if ((size_t)a.N * K64 * 64 <= kRowSplitWeightBytes) return go(std::integral_constant<int, 4>{});
-    go(std::integral_constant<int, 16>{});
+        if ((size_t)a.N * K64 * 64 <= kRowSplitWeightBytes) {
+            // 12 features per workgroup when 16 leave CUs idle and 12 fill
+            // them (N = 768, 16 rows: 192 -> 256 workgroups)
+            const long long rb = (a.M + 3) / 4, cus = num_cus();
+            if ((long long)blocks * rb < cus && (long long)((a.N + 11) / 12) * rb <= cus)
+                return go(std::integral_constant<int, 4>{}, std::integral_constant<int, 12>{});
+            return go(std::integral_constant<int, 4>{}, std::integral_constant<int, 16>{});
+        }
+    go(std::integral_constant<int, 16>{}, std::integral_constant<int, 16>{});
 }
 
 template <int EPI>
