@@ -109,7 +109,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     constexpr int NJ = 4 / (NW / 4);        // 32-column blocks per wave: 4 or 2
     constexpr int LOADS_PER_WAVE = BM / ROWS_PER_LOAD / NW;  // per operand per stage
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform, so the copies' LDS destinations (M0) are scalar arithmetic
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
 
     i32x16 acc[4][NJ];
