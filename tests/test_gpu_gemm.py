@@ -154,6 +154,25 @@ def test_k8192_gemv_epilogues(ie, orc, epi, M, N):
         assert np.array_equal(got, want), np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 700, 768), (6, 13, 3072), (9, 1000, 768), (16, 768, 3072)])
+@pytest.mark.parametrize("epi", [0, 1, 3])
+def test_mfma_gemv_twelve_feature_workgroups(ie, orc, M, N, K, epi):
+    """Small N at 5 <= M <= 16: the MFMA GEMV takes 12 features per workgroup
+    when 16 would leave CUs idle and 12 fill them (columns 12-15 of each
+    workgroup re-read its feature 11 and are not stored), including a
+    partial last workgroup (N = 700, 13, 1000); bit-exact."""
+    A, W = problem(M, N, K, 41 * M + N + K + epi)
+    r = rng(77 + epi)
+    bias = (r.standard_normal(N) * 0.5).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi,
+                            dev(bias) if epi else None, dev(res) if epi == 3 else None, path=ie.PATH_GEMV))
+    want = orc.gemm(Ap, Wp, sA, sW, epi, bias if epi else None, res if epi == 3 else None)
+    assert np.array_equal(got, want), np.abs(got - want).max()
+
+
 # ------------------------------------------------------------------ epilogues
 @pytest.mark.parametrize("M,K,N,path", [(1, 768, 2304, 1), (16, 3072, 768, 1), (4, 768, 3072, 1),
                                         (64, 768, 2304, 2), (512, 3072, 768, 2), (16, 768, 768, 2)])
