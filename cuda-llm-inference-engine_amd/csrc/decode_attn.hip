@@ -66,8 +66,9 @@ constexpr int kCpolNT = 2;
 // elements need the registers).  G = 8 at d = 128 holds 8 heads' q and o per
 // wave, so it takes 4 waves per workgroup (one per SIMD, all registers) and
 // the pair: at 8 waves, or with a four-chunk fp32 ring, it spilled and ran at
-// 0.15-0.25 of HBM peak against 0.52-0.66 (fp32) and 0.35-0.40 (bf16) now,
-// ctx 4096-32768 (a three-chunk bf16 ring measured 7% slower).
+// 0.15-0.25 of HBM peak against 0.52-0.66 (fp32 then; 0.68-0.70 at ctx 8192
+// with v_exp_f32 weights and scalar block ids), and a three-chunk fp32 ring
+// spills too.  bf16 at G >= 4 takes the MFMA walk below.
 template <int D, typename KV, int G>
 constexpr int wave_heads() { return (D == 128 && sizeof(KV) == 4) || (D == 128 && G == 8) ? 4 : 8; }
 template <int D, typename KV, int G>
