@@ -366,11 +366,13 @@ def test_cfg2_m512_lm_head_shape_full(ie, orc, epi):
 
 # ------------------------------------------------------------------ 256x256 tiles
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (3000, 5000, 512), (2304, 8192, 768),
-                                   (8192, 3000, 256)])
+                                   (8192, 3000, 256), (4096, 8448, 384), (4352, 4352, 640)])
 def test_big_tile_kernel_exact(ie, orc, M, N, K):
     """Shapes routed to the 256x256-tile kernel (>= 128 tiles, K % 128 == 0),
-    including ragged M and N; int32 exact on sampled rows plus a full column
-    checksum."""
+    including ragged M and N; more tiles than CUs, so persistent workgroups
+    take several tiles each (one whose next tile's first K stage lands in the
+    other LDS slot: an odd number of K stages, K = 384 and 640); int32 exact
+    on sampled rows plus a full column checksum."""
     import torch
 
     gen = torch.Generator(device="cuda").manual_seed(M + N + K)
