@@ -7,6 +7,7 @@ is rejected, it raises.
 from __future__ import annotations
 
 import ctypes
+import numbers
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -69,6 +70,17 @@ ENGINE_SIGNATURES = {
 }
 
 
+# include/ie_tokenizer.h (host code; no GPU)
+TOKENIZER_SIGNATURES = {
+    "ie_tokenizer_create": (_I, [_P, ctypes.c_char_p]),
+    "ie_tokenizer_destroy": (_I, [_P]),
+    "ie_tokenizer_encode": (_I, [_P, ctypes.c_char_p, _Z, _P, _Z, _P]),
+    "ie_tokenizer_decode": (_I, [_P, _P, _Z, _P, _Z, _P]),
+    "ie_tokenizer_vocab_size": (_I, [_P]),
+    "ie_tokenizer_eos_token": (_I, [_P]),
+}
+
+
 class Metrics(ctypes.Structure):
     """ie_metrics (include/ie_engine.h): InferenceMetrics without `generating`."""
     _fields_ = [(n, ctypes.c_float) for n in ("ttft_ms", "tpot_ms", "itl_min_ms", "itl_max_ms",
@@ -108,7 +120,8 @@ def load() -> ctypes.CDLL:
                 f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
                 "(make -C cuda-llm-inference-engine_amd)")
         lib = ctypes.CDLL(LIB_PATH)
-        for name, (res, args) in list(SIGNATURES.items()) + list(ENGINE_SIGNATURES.items()):
+        for name, (res, args) in (list(SIGNATURES.items()) + list(ENGINE_SIGNATURES.items())
+                                  + list(TOKENIZER_SIGNATURES.items())):
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
@@ -402,8 +415,66 @@ class Engine:
               ctypes.byref(n), ctypes.byref(m))
         return out[: n.value].tolist(), m.as_dict()
 
+    def generate_text(self, tokenizer, prompt, max_new, temperature=0.8, top_k=40, greedy=False, reset=True):
+        """The reference's text path (src/main.cpp:224-230, 360-367): the prompt
+        encoded by the BPE tokenizer, GPT2Engine::generate, the ids decoded ->
+        (generated bytes, generated ids, metrics dict)."""
+        ids = tokenizer.encode(prompt)
+        if not ids:
+            raise ValueError("the prompt encodes to no tokens")
+        toks, m = self.generate_one(ids, max_new, temperature, top_k, greedy, reset)
+        return tokenizer.decode(toks), toks, m
+
     def session_tokens(self):
         return load().ie_engine_session_tokens(self.h)
 
     def step_bytes(self, batch):
         return load().ie_engine_step_bytes(self.h, batch)
+
+
+class Tokenizer:
+    """GPT-2 byte-level BPE tokenizer (include/ie_tokenizer.h), the reference's
+    BPETokenizer (include/tokenizer.h:7-25): vocab.json and merges.txt from
+    model_dir.  encode takes str or bytes; decode returns bytes, since a token
+    can end inside a multi-byte character."""
+
+    def __init__(self, model_dir):
+        h = ctypes.c_void_p()
+        check("ie_tokenizer_create", ctypes.byref(h), os.fsencode(model_dir))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            load().ie_tokenizer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode(self, text):
+        b = text.encode("utf-8") if isinstance(text, str) else bytes(text)
+        n = ctypes.c_size_t()
+        check("ie_tokenizer_encode", self.h, b, len(b), None, 0, ctypes.byref(n))
+        out = (ctypes.c_int * max(n.value, 1))()
+        check("ie_tokenizer_encode", self.h, b, len(b), out, n.value, ctypes.byref(n))
+        return list(out[:n.value])
+
+    def decode(self, ids):
+        ids = [int(i) for i in ([ids] if isinstance(ids, numbers.Integral) else ids)]
+        arr = (ctypes.c_int * max(len(ids), 1))(*ids)
+        n = ctypes.c_size_t()
+        check("ie_tokenizer_decode", self.h, arr, len(ids), None, 0, ctypes.byref(n))
+        buf = ctypes.create_string_buffer(max(n.value, 1))
+        check("ie_tokenizer_decode", self.h, arr, len(ids), buf, n.value, ctypes.byref(n))
+        return buf.raw[:n.value]
+
+    @property
+    def vocab_size(self):
+        return load().ie_tokenizer_vocab_size(self.h)
+
+    @property
+    def eos_token(self):
+        return load().ie_tokenizer_eos_token(self.h)

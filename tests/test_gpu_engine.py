@@ -483,3 +483,31 @@ def test_greedy_ties_take_the_lowest_index(ie, tmp_path):
         out, _ = eng.generate(prompts, 4, ignore_eos=True)
         assert (out == 5000).all(), (kw, out)
         eng.close()
+
+
+def test_text_prompt_path(ie, tmp_path):
+    """The reference's text path (src/main.cpp:224-230): the prompt encoded by
+    the BPE tokenizer from the model directory's vocab.json / merges.txt,
+    generated from, and the ids decoded; the echo law gives the ids."""
+    import json
+
+    from oracle.bpe_tokenizer import byte_table
+
+    d = tmp_path / "echo"
+    t = echo_model(d, 40)
+    sym = byte_table()
+    vocab = {sym[b]: b for b in range(256)}
+    vocab.update({"He": 256, "llo": 257, "Hello": 258, sym[0x20] + "world": 259, "<|endoftext|>": EOS})
+    merges = [("H", "e"), ("l", "l"), ("ll", "o"), ("He", "llo"), (sym[0x20], "w"), (sym[0x20] + "w", "o"),
+              (sym[0x20] + "wo", "r"), (sym[0x20] + "wor", "l"), (sym[0x20] + "worl", "d")]
+    (d / "vocab.json").write_text(json.dumps(vocab))
+    (d / "merges.txt").write_text("#version: 0.2\n" + "".join(f"{a} {b}\n" for a, b in merges), encoding="utf-8")
+    tok = ie.Tokenizer(d)
+    text = "Hello world, says the\techo"
+    ids = tok.encode(text)
+    assert ids[:2] == [258, 259] and tok.decode(ids) == b"Hello world, says the echo"
+    eng = ie.Engine(d, max_batch=1)
+    out, got, m = eng.generate_text(tok, text, 64, greedy=True)
+    want = echo_expected(t, ids[-1], len(ids) - 1, 64)
+    assert got == want and out == tok.decode(want) and m["tokens_generated"] == len(want)
+    eng.close()
