@@ -204,3 +204,38 @@ def test_errors(ie, tmp_path):
     lib = ie.load()
     assert lib.ie_tokenizer_create(None, b"x") == ie.IE_ERR_INVALID
     assert lib.ie_tokenizer_vocab_size(None) == -1
+
+
+def test_cpp_class_drop_in(ie, trained_dir, tmp_path):
+    """src/main.cpp's use of BPETokenizer (src/main.cpp:224-230, 355-367),
+    compiled against include/ie_bpe_tokenizer.h and linked with libie_amd.so:
+    the ids and text match the oracle's, and a missing directory throws."""
+    import subprocess
+
+    d, _, words = trained_dir
+    text = " ".join(words[:40]) + " \\ ] x"
+    src = r"""
+#include "ie_bpe_tokenizer.h"
+#include <cstdio>
+#include <stdexcept>
+int main(int argc, char** argv) {
+    BPETokenizer tokenizer(argv[1]);
+    std::vector<int> ids = tokenizer.encode(argv[2]);
+    for (int id : ids) printf("%d ", id);
+    printf("\n%s\n%d %d\n", tokenizer.decode(ids).c_str(), tokenizer.vocab_size(), tokenizer.eos_token());
+    try { BPETokenizer missing(std::string(argv[1]) + "/nowhere"); } catch (const std::runtime_error&) { return 0; }
+    return 3;
+}
+"""
+    cpp, exe = str(tmp_path / "t.cpp"), str(tmp_path / "t")
+    open(cpp, "w").write(src)
+    subprocess.run(["g++", "-std=c++17", "-I", os.path.join(ROOT, "include"), cpp, "-o", exe, ie.LIB_PATH,
+                    f"-Wl,-rpath,{os.path.dirname(ie.LIB_PATH)}"], check=True)
+    r = subprocess.run([exe, d, text], capture_output=True)
+    assert r.returncode == 0, (r.returncode, r.stderr)
+    lines = r.stdout.split(b"\n")
+    o = OracleBPE(d)
+    want = o.encode(text.encode())
+    assert [int(x) for x in lines[0].split()] == want and 59 in want and 60 in want
+    assert lines[1] == o.decode(want) == text.encode()
+    assert lines[2] == f"{TABLE_IDS} {EOS}".encode()
