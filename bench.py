@@ -330,14 +330,42 @@ def bench_attn(ie):
 # (README.md:162-169, 183-186; benchmarks/int8_gemm_bench.cu:27,
 # benchmarks/decode_attention_bench.cu:57-67): context only, other hardware.
 REF_GEMM_US = {256: 23.7, 512: 93.2, 1024: 788.3, 2048: 5213.2}
+# the same table's FP32 cuBLAS column on the reference's GPU (README.md:181-186)
+REF_FP32_US = {256: 31.8, 512: 212.8, 1024: 963.2, 2048: 6619.3}
 REF_ATTN_US = [((1, 8, 8, 128), 31.9), ((1, 8, 8, 256), 25.2), ((1, 8, 8, 512), 29.5), ((1, 8, 8, 1024), 51.8),
                ((4, 8, 8, 256), 49.0), ((8, 8, 8, 512), 162.6), ((1, 16, 4, 256), 34.9), ((1, 32, 8, 512), 81.5)]
+
+
+def vendor_sgemm_us(A, B, C, reps=20):
+    """fp32 C = A @ B on the vendor BLAS, the reference bench's cuBLAS SGEMM
+    column (benchmarks/int8_gemm_bench.cu:78-96): 3 warm-ups, then `reps`
+    back-to-back launches between HIP events.  rocBLAS (torch's "cublas"
+    backend on ROCm) and hipBLASLt ("cublaslt")."""
+    import torch
+
+    be = torch.backends.cuda.preferred_blas_library()
+    res = {}
+    try:
+        for name, lib in (("rocblas", "cublas"), ("hipblaslt", "cublaslt")):
+            torch.backends.cuda.preferred_blas_library(lib)
+            for _ in range(3):
+                torch.mm(A, B, out=C)
+            torch.cuda.synchronize()
+            with Timer() as t:
+                for _ in range(reps):
+                    torch.mm(A, B, out=C)
+            res[name] = t.ms * 1e3 / reps
+    finally:
+        torch.backends.cuda.preferred_blas_library(be)
+    return res
 
 
 def bench_ref_shapes(ie):
     """INT8 GEMM S^3 (U(-1,1) operands quantized by the library, Plain
     epilogue; 512^3 is BASELINE cfg1) and decode attention (d 64, block 16,
-    fp32, every sequence at ctx), timed from HIP graphs."""
+    fp32, every sequence at ctx), timed from HIP graphs.  Beside each GEMM,
+    as the reference bench prints it: the fp32 vendor GEMM on the same
+    operands (rocBLAS SGEMM; hipBLASLt too) and the FP32/INT8 time ratio."""
     import torch
 
     out = {"gemm": [], "decode_attn": [], "reference_hw": "GTX 1650 Ti (README.md:28-30)"}
@@ -351,6 +379,17 @@ def bench_ref_shapes(ie):
         ms = graph_time(lambda i: ie.int8_gemm(Ap, Bp, sA, sB, ie.EPI_PLAIN, out=C), 20)
         r = {"M=N=K": S, "us": round(ms * 1e3, 2), "TOPs": round(2.0 * S ** 3 / (ms * 1e-3) / 1e12, 2),
              "reference_us": ref_us}
+        try:
+            B = BT.t().contiguous()
+            fp = vendor_sgemm_us(A, B, torch.empty((S, S), device="cuda"))
+            r["fp32_rocblas_us"] = round(fp["rocblas"], 2)
+            r["fp32_hipblaslt_us"] = round(fp["hipblaslt"], 2)
+            r["int8_over_fp32"] = round(fp["rocblas"] / (ms * 1e3), 2)  # the reference's INT8/FP32 column
+            r["reference_fp32_us"] = REF_FP32_US[S]
+            r["reference_int8_over_fp32"] = round(REF_FP32_US[S] / ref_us, 2)
+            del B
+        except Exception as e:  # noqa: BLE001 - reported, not fatal
+            r["fp32_error"] = str(e)[:200]
         out["gemm"].append(r)
         log(f"ref gemm {r}")
     for (B, H_q, H_kv, ctx), ref_us in REF_ATTN_US:

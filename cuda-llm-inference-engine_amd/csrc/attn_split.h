@@ -227,14 +227,18 @@ struct SplitWalk {
         kbase = (OPQ ? opaque_global(kcache) : kcache) + (size_t)kvh * D + li * EPL;
         vbase = (OPQ ? opaque_global(vcache) : vcache) + (size_t)kvh * D + li * EPL;
         c0 = tok0 + wave * CT;
+        any = c0 < tok1;
         if constexpr (BS16) {
             static_assert(NPH == 1, "a chunk lies in one block");
+            // An empty walk reads no table entry: with tok1 == 0 the clamp in
+            // phys() would index bt[-1], and an empty row may have no entries.
             if (pn0 >= 0)
                 pn[0] = pn0;
-            else
+            else if (any)
                 prefetch(c0);
+            else
+                pn[0] = 0;
         }
-        any = c0 < tok1;
         if (any) {
 #pragma unroll
             for (int p = 0; p < R - 1; ++p) next(buf[p], c0 + p * STEP);

@@ -297,6 +297,17 @@ int ie_layernorm(int rows, int cols, const float* x, const float* gamma, const f
     return ie::check_launch("layernorm");
 }
 
+int ie_layernorm_residual(int rows, int cols, const float* x, const float* residual, const float* gamma,
+                          const float* beta, float* out, float* residual_out, float eps, ie_stream_t stream) {
+    if (rows < 0 || cols <= 0) return ie::fail(IE_ERR_INVALID, "layernorm_residual: bad sizes");
+    if (rows == 0) return IE_OK;
+    if (!x || !residual || !gamma || !beta || !out || !residual_out)
+        return ie::fail(IE_ERR_INVALID, "layernorm_residual: null pointer");
+    ie::launch_layernorm_residual(rows, cols, x, residual, gamma, beta, out, residual_out, eps,
+                                  (hipStream_t)stream);
+    return ie::check_launch("layernorm_residual");
+}
+
 int ie_embedding(const int* token_ids, int seq_len, int start_pos, int d_model, const float* wte,
                  const float* wpe, float* out, ie_stream_t stream) {
     if (seq_len < 0 || start_pos < 0 || d_model <= 0) return ie::fail(IE_ERR_INVALID, "embedding: bad sizes");

@@ -76,6 +76,13 @@ void run_layernorm(int rows, int cols, const float* x, const float* gamma, const
     report("run_layernorm", ie_layernorm(rows, cols, x, gamma, beta, out, eps, nullptr));
 }
 
+// kernels/layernorm/15_layernorm_residual.cuh:7-15
+void run_layernorm_residual(int rows, int cols, const float* x, const float* residual, const float* gamma,
+                            const float* beta, float* out, float* residual_out, float eps) {
+    report("run_layernorm_residual",
+           ie_layernorm_residual(rows, cols, x, residual, gamma, beta, out, residual_out, eps, nullptr));
+}
+
 // kernels/layernorm/15_embed.cuh
 void run_embedding(const int* token_ids, int seq_len, int start_pos, int d_model,
                    const float* wte, const float* wpe, float* out) {

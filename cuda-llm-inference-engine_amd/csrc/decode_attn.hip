@@ -192,7 +192,8 @@ __device__ __forceinline__ void split_partial_klds(const float* __restrict__ Q, 
     int c0 = tok0;
     // the chunk's block id is wave-uniform: a scalar load, counted by lgkmcnt
     auto phys = [&](int cs) { return bt[__builtin_amdgcn_readfirstlane(min(cs, tok1 - 1) >> 4)]; };
-    int pn = phys(c0);
+    // an empty walk reads no table entry (tok1 == 0 would index bt[-1])
+    int pn = c0 < tok1 ? phys(c0) : 0;
     // Issues chunk cs: K pieces into ring slot `slot`, then V into vb.
     auto issue = [&](VChunk& vb, int slot, int cs) {
         const int ph = pn;

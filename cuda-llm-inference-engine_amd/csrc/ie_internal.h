@@ -179,6 +179,9 @@ void launch_fp32_epilogue(int M, int N, const float* g, const float* bias, const
 // ---- support ops (support.hip) ----
 void launch_layernorm(int rows, int cols, const float* x, const float* g,
                       const float* b, float* out, float eps, hipStream_t s);
+// residual_out = x + res, out = LayerNorm(residual_out); any aliasing allowed.
+void launch_layernorm_residual(int rows, int cols, const float* x, const float* res, const float* g,
+                               const float* b, float* out, float* res_out, float eps, hipStream_t s);
 void launch_embedding(const int* ids, int seq_len, int start_pos, int d,
                       const float* wte, const float* wpe, float* out,
                       hipStream_t s);

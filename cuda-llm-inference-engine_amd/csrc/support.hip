@@ -47,6 +47,58 @@ __global__ __launch_bounds__(256) void layernorm_kernel(int rows, int cols, cons
     }
 }
 
+// kernels/layernorm/15_layernorm_residual.cu:6-57: y = x + residual (one fp32
+// add), residual_out = y, out = LayerNorm(y) with the standalone LayerNorm's
+// reduction order (ln_accum / ln_finish / ln_apply), so out equals
+// layernorm(residual_out) bit for bit.  As in the reference, any of out and
+// residual_out may alias x or residual (or each other): a lane reads an
+// element's x and residual before it writes that element, and the second pass
+// reads y back from residual_out, which the same lane wrote.
+template <bool VEC>
+__global__ __launch_bounds__(256) void layernorm_residual_kernel(int rows, int cols, const float* x,
+                                                                 const float* res,
+                                                                 const float* __restrict__ gamma,
+                                                                 const float* __restrict__ beta,
+                                                                 float* out, float* res_out, float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const size_t off = (size_t)row * cols;
+    float s = 0.0f, s2 = 0.0f, mean, rs;
+    if constexpr (VEC) {
+        const int n4 = cols >> 2;
+        const float4* x4 = reinterpret_cast<const float4*>(x + off);
+        const float4* r4 = reinterpret_cast<const float4*>(res + off);
+        float4* y4 = reinterpret_cast<float4*>(res_out + off);
+        for (int j = lane; j < n4; j += 64) {
+            const float4 a = x4[j], b = r4[j];
+            const float4 y = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+            y4[j] = y;
+            ln_accum(y, s, s2);
+        }
+        ln_finish(s, s2, cols, eps, mean, rs);
+        const float4* g4 = reinterpret_cast<const float4*>(gamma);
+        const float4* b4 = reinterpret_cast<const float4*>(beta);
+        float4* o4 = reinterpret_cast<float4*>(out + off);
+        for (int j = lane; j < n4; j += 64) {
+            const float4 y = y4[j];
+            o4[j] = ln_apply(y, g4[j], b4[j], mean, rs);
+        }
+    } else {
+        for (int c = lane; c < cols; c += 64) {
+            const float v = x[off + c] + res[off + c];
+            res_out[off + c] = v;
+            s += v;
+            s2 = fmaf(v, v, s2);
+        }
+        ln_finish(s, s2, cols, eps, mean, rs);
+        for (int c = lane; c < cols; c += 64) {
+            const float v = res_out[off + c];
+            out[off + c] = fmaf(gamma[c] * (v - mean), rs, beta[c]);
+        }
+    }
+}
+
 // kernels/layernorm/15_embed.cu:4-21.
 __global__ __launch_bounds__(256) void embedding_kernel(const int* __restrict__ ids, int seq_len,
                                                         int start_pos, int d,
@@ -485,6 +537,18 @@ void launch_layernorm(int rows, int cols, const float* x, const float* g, const 
         layernorm_kernel<true><<<blocks, 256, 0, s>>>(rows, cols, x, g, b, out, eps);
     else
         layernorm_kernel<false><<<blocks, 256, 0, s>>>(rows, cols, x, g, b, out, eps);
+}
+
+void launch_layernorm_residual(int rows, int cols, const float* x, const float* res, const float* g,
+                               const float* b, float* out, float* res_out, float eps, hipStream_t s) {
+    if (rows == 0) return;
+    const bool vec = cols % 4 == 0 && (((uintptr_t)x | (uintptr_t)res | (uintptr_t)g | (uintptr_t)b |
+                                        (uintptr_t)out | (uintptr_t)res_out) % 16) == 0;
+    const unsigned blocks = (unsigned)((rows + 3) / 4);
+    if (vec)
+        layernorm_residual_kernel<true><<<blocks, 256, 0, s>>>(rows, cols, x, res, g, b, out, res_out, eps);
+    else
+        layernorm_residual_kernel<false><<<blocks, 256, 0, s>>>(rows, cols, x, res, g, b, out, res_out, eps);
 }
 
 void launch_embedding(const int* ids, int seq_len, int start_pos, int d, const float* wte,

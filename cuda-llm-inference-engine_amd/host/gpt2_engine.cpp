@@ -444,6 +444,9 @@ struct GPT2Engine::Impl {
     }
 
     ~Impl() {  // best effort: a destructor has nowhere to report errors
+        // the rocBLAS handle is bound to `stream` and may free its workspace
+        // on it: release it while the stream and the buffers still exist
+        blas.reset();
         for (auto& kv : graphs)
             if (kv.second) (void)hipGraphExecDestroy(kv.second);
         for (void* p : allocs) (void)hipFree(p);
@@ -1091,9 +1094,11 @@ void GPT2Engine::generate_batch(const std::vector<std::vector<int>>& prompts, in
         // The step for this iteration was enqueued unless a limit other than
         // EOS ruled it out: stop here as the step-by-step loop would.
         if (all_done || pipe.launched == pipe.waited) break;
-        for (int b = 0; b < B; ++b) decode_tokens += done[b] ? 0 : 1;
         if (stepi + 2 < max_new_tokens && I.pos < I.cfg.max_seq_len) pipe.launch();
         const int* ids = pipe.wait();
+        // The timed step's tokens: one for each sequence still running when
+        // it was enqueued (done[] does not yet see the ids it returned).
+        for (int b = 0; b < B; ++b) decode_tokens += done[b] ? 0 : 1;
         std::copy(ids, ids + B, cur.begin());
         const auto now = Clock::now();
         const float dt = std::chrono::duration<float, std::milli>(now - t).count();

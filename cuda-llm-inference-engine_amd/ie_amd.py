@@ -42,6 +42,7 @@ SIGNATURES = {
     "ie_kv_cache_write": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P]),
     "ie_kv_cache_append_batch": (_I, [_I, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _P]),
     "ie_layernorm": (_I, [_I, _I, _P, _P, _P, _P, _F, _P]),
+    "ie_layernorm_residual": (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _F, _P]),
     "ie_embedding": (_I, [_P, _I, _I, _I, _P, _P, _P, _P]),
     "ie_embedding_batch": (_I, [_I, _P, _P, _I, _P, _P, _P, _P]),
     "ie_vocab_proj": (_I, [_I, _P, _P, _P, _I, _I, _P]),
@@ -273,6 +274,19 @@ def layernorm(x, gamma, beta, out=None, eps=1e-5, stream=None):
     out = out if out is not None else torch.empty_like(x)
     check("ie_layernorm", rows, cols, _ptr(x), _ptr(gamma), _ptr(beta), _ptr(out), eps, _stream(stream))
     return out
+
+
+def layernorm_residual(x, residual, gamma, beta, out=None, residual_out=None, eps=1e-5, stream=None):
+    """(LayerNorm(x + residual), x + residual); out / residual_out may alias
+    the inputs."""
+    import torch
+
+    rows, cols = x.shape
+    out = out if out is not None else torch.empty_like(x)
+    residual_out = residual_out if residual_out is not None else torch.empty_like(x)
+    check("ie_layernorm_residual", rows, cols, _ptr(x), _ptr(residual), _ptr(gamma), _ptr(beta), _ptr(out),
+          _ptr(residual_out), eps, _stream(stream))
+    return out, residual_out
 
 
 def embedding(ids, start_pos, wte, wpe, out=None, stream=None):

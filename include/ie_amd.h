@@ -22,6 +22,8 @@
  *   ie_kv_cache_write         kv_cache_write_kernel / GPT2Engine::kv_cache_append
  *                             src/gpt2_engine.cu:321-346, 431-445
  *   ie_layernorm              run_layernorm  kernels/layernorm/15_layernorm_residual.cu:120-130
+ *   ie_layernorm_residual     run_layernorm_residual
+ *                             kernels/layernorm/15_layernorm_residual.cuh:7-15, .cu:6-57,105-118
  *   ie_embedding              run_embedding  kernels/layernorm/15_embed.cu:24-30
  *   ie_vocab_proj             run_vocab_proj src/gpt2_engine.cu:391-410
  *   ie_argmax                 sample_argmax  src/sampler.cu:10-14 (device-side)
@@ -183,6 +185,14 @@ int ie_kv_cache_append_batch(int B, const float* K_src, const float* V_src,
 /* Support operations of the decode step. */
 int ie_layernorm(int rows, int cols, const float* x, const float* gamma,
                  const float* beta, float* out, float eps, ie_stream_t stream);
+/* residual_out = x + residual (one fp32 add per element), out =
+ * LayerNorm(residual_out) with ie_layernorm's arithmetic (so out equals
+ * ie_layernorm of residual_out bit for bit).  [rows, cols] row-major; out and
+ * residual_out may alias x, residual or each other, as in the reference. */
+int ie_layernorm_residual(int rows, int cols, const float* x,
+                          const float* residual, const float* gamma,
+                          const float* beta, float* out, float* residual_out,
+                          float eps, ie_stream_t stream);
 int ie_embedding(const int* token_ids, int seq_len, int start_pos,
                  int d_model, const float* wte, const float* wpe, float* out,
                  ie_stream_t stream);

@@ -6,7 +6,8 @@
  *   kernels/quantization/14_int8_gemm.cuh:20-64   quantizer, INT8 GEMM, epilogues
  *   kernels/decode/13_decode_attn.cuh:12,192-199   DA_MAX_SPLITS, run_decode_attn
  *   kernels/flash_attention/10_flash_attn_v2.cuh   run_flash_attn_v2
- *   kernels/layernorm/15_layernorm_residual.cuh    run_layernorm
+ *   kernels/quantization/14_int8_gemm.cuh:11-16    I8_BM ... I8_NTHREADS
+ *   kernels/layernorm/15_layernorm_residual.cuh    run_layernorm_residual, run_layernorm
  *   kernels/layernorm/15_embed.cuh                 run_embedding
  *   include/sampler.cuh                            sample_argmax, sample_top_k
  *
@@ -22,6 +23,18 @@
 #include <cstdint>
 
 #include "ie_amd.h"
+
+/* The reference K14 kernel's tile constants (its 64x64 tile, 16-byte K step,
+ * 4x4 thread tile, 256 threads), kept for callers that print or size with
+ * them, e.g. the reference's INT8 bench header line.  They describe the
+ * reference's kernel, not this library's tiling (MFMA tiles chosen per
+ * shape), and size nothing a caller passes to it. */
+#define I8_BM 64
+#define I8_BN 64
+#define I8_BK 16
+#define I8_TM 4
+#define I8_TN 4
+#define I8_NTHREADS 256
 
 /* Workspace sizing used by callers of run_decode_attn:
  * [B, H_q, DA_MAX_SPLITS, d + 2] floats (src/gpt2_engine.cu:156). */
@@ -60,6 +73,13 @@ void run_decode_attn(int B, int H_q, int H_kv, int d, const float* Q,
  * overlapping call is reported and leaves O untouched). */
 void run_flash_attn_v2(int B, int H, int N, int d, const float* Q,
                        const float* K, const float* V, float* O, bool causal);
+
+/* out = LayerNorm(x + residual), residual_out = x + residual; out and
+ * residual_out may alias the inputs. */
+void run_layernorm_residual(int rows, int cols, const float* x,
+                            const float* residual, const float* gamma,
+                            const float* beta, float* out, float* residual_out,
+                            float eps = 1e-5f);
 
 void run_layernorm(int rows, int cols, const float* x, const float* gamma,
                    const float* beta, float* out, float eps = 1e-5f);

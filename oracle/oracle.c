@@ -481,6 +481,16 @@ void orc_layernorm(int rows, int cols, const float* x, const float* gamma,
     }
 }
 
+/* 15_layernorm_residual.cu:6-57: y = x + residual in fp32 (one rounding),
+ * residual_out = y, out = orc_layernorm(y).  residual_out may alias x or
+ * residual (each element is read before it is written). */
+void orc_layernorm_residual(int rows, int cols, const float* x, const float* residual,
+                            const float* gamma, const float* beta, float* out,
+                            float* residual_out, float eps) {
+    for (size_t i = 0; i < (size_t)rows * cols; ++i) residual_out[i] = x[i] + residual[i];
+    orc_layernorm(rows, cols, residual_out, gamma, beta, out, eps);
+}
+
 void orc_embedding(const int* token_ids, int seq_len, int start_pos,
                    int d_model, const float* wte, const float* wpe, float* out) {
     for (int t = 0; t < seq_len; ++t)

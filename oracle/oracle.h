@@ -25,6 +25,9 @@
  *                             table permutation invariance, split invariance
  *   orc_kv_cache_write        closed-form index map (numpy fancy indexing)
  *   orc_layernorm             torch layer_norm in fp64
+ *   orc_layernorm_residual    numpy fp32 add, torch layer_norm in fp64 of the
+ *                             sum; not LN(x) + residual nor LN(residual); the
+ *                             reference test's own srand(42) cases and bound
  *   orc_embedding, orc_vocab_proj, orc_argmax
  *                             numpy gather / matmul / argmax
  *   orc_topk                  Python sorted() by (-value, index) brute force,
@@ -110,6 +113,10 @@ int orc_kv_cache_write(const float* K_src, const float* V_src, float* k_cache,
 /* kernels/layernorm/15_layernorm_residual.cu:59-103 */
 void orc_layernorm(int rows, int cols, const float* x, const float* gamma,
                    const float* beta, float* out, float eps);
+/* kernels/layernorm/15_layernorm_residual.cu:6-57 */
+void orc_layernorm_residual(int rows, int cols, const float* x, const float* residual,
+                            const float* gamma, const float* beta, float* out,
+                            float* residual_out, float eps);
 /* kernels/layernorm/15_embed.cu:4-21 */
 void orc_embedding(const int* token_ids, int seq_len, int start_pos,
                    int d_model, const float* wte, const float* wpe, float* out);

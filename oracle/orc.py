@@ -36,6 +36,7 @@ SIGNATURES = {
     "orc_decode_attn_f32": (_I, [_I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P]),
     "orc_kv_cache_write": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "orc_layernorm": (None, [_I, _I, _P, _P, _P, _P, _F]),
+    "orc_layernorm_residual": (None, [_I, _I, _P, _P, _P, _P, _P, _P, _F]),
     "orc_embedding": (None, [_P, _I, _I, _I, _P, _P, _P]),
     "orc_vocab_proj": (None, [_P, _P, _P, _I, _I]),
     "orc_argmax": (_I, [_P, _I]),
@@ -192,6 +193,19 @@ def layernorm(x, gamma, beta, eps=1e-5):
     load().orc_layernorm(rows, cols, _p(x), _p(_c(gamma, np.float32)), _p(_c(beta, np.float32)),
                          _p(out), eps)
     return out
+
+
+def layernorm_residual(x, residual, gamma, beta, eps=1e-5):
+    """-> (LayerNorm(x + residual), x + residual)."""
+    x = _c(x, np.float32)
+    residual = _c(residual, np.float32)
+    assert x.shape == residual.shape
+    rows, cols = x.shape
+    out = np.empty_like(x)
+    res_out = np.empty_like(x)
+    load().orc_layernorm_residual(rows, cols, _p(x), _p(residual), _p(_c(gamma, np.float32)),
+                                  _p(_c(beta, np.float32)), _p(out), _p(res_out), eps)
+    return out, res_out
 
 
 def embedding(ids, start_pos, wte, wpe):

@@ -13,6 +13,11 @@
 //   run_layernorm in place (the engine's use, src/gpt2_engine.cu:459),
 //   run_embedding, run_flash_attn_v2 (causal and not), sample_argmax and
 //   sample_top_k.
+//   run_layernorm_residual: tests/test_layernorm.cu:34-70 on its five shapes
+//     (srand(42): x, residual, gamma in [0.8, 1.2], beta in [-0.1, 0.1]),
+//     separate outputs, then again in place (out over x, residual_out over
+//     the residual).
+//   The K14 tile constants printed as benchmarks/int8_gemm_bench.cu:17 does.
 //
 // Every input and output is written to <out_dir>/<case>_<name>.bin (raw
 // little-endian), and one line per case to <out_dir>/manifest.txt; the
@@ -172,6 +177,34 @@ void attn_case(int B, int H_q, int H_kv, int ctx, int d, int bs) {
         hip_ok(hipFree(p), "hipFree");
 }
 
+// tests/test_layernorm.cu:34-70.
+void layernorm_residual_case(int rows, int cols) {
+    char cs[64];
+    std::snprintf(cs, sizeof(cs), "lnr_%d_%d", rows, cols);
+    const size_t n = (size_t)rows * cols;
+    std::vector<float> x(n), res(n), gamma(cols), beta(cols);
+    srand(42);
+    for (auto& v : x) v = (float)rand() / RAND_MAX * 2.0f - 1.0f;
+    for (auto& v : res) v = (float)rand() / RAND_MAX * 2.0f - 1.0f;
+    for (auto& v : gamma) v = 0.8f + (float)rand() / RAND_MAX * 0.4f;
+    for (auto& v : beta) v = (float)rand() / RAND_MAX * 0.2f - 0.1f;
+    float *dx = upload(x), *dres = upload(res), *dg = upload(gamma), *db = upload(beta);
+    float *dout = dalloc<float>(n), *dres_out = dalloc<float>(n);
+    run_layernorm_residual(rows, cols, dx, dres, dg, db, dout, dres_out);
+    save(cs, "out", download(dout, n));
+    save(cs, "res_out", download(dres_out, n));
+    run_layernorm_residual(rows, cols, dx, dres, dg, db, dx, dres);  // in place
+    save(cs, "out_inplace", download(dx, n));
+    save(cs, "res_out_inplace", download(dres, n));
+    save(cs, "x", x);
+    save(cs, "res", res);
+    save(cs, "gamma", gamma);
+    save(cs, "beta", beta);
+    std::fprintf(g_manifest, "lnres %s %d %d\n", cs, rows, cols);
+    for (void* p : {(void*)dx, (void*)dres, (void*)dg, (void*)db, (void*)dout, (void*)dres_out})
+        hip_ok(hipFree(p), "hipFree");
+}
+
 void support_cases() {
     // run_layernorm in place: x and out are the same buffer
     const int rows = 4, cols = 768;
@@ -248,6 +281,9 @@ int main(int argc, char** argv) {
     g_dir = argv[1];
     g_manifest = std::fopen((g_dir + "/manifest.txt").c_str(), "w");
     if (!g_manifest) return 4;
+    // benchmarks/int8_gemm_bench.cu:16-17
+    std::printf("Tile: BM=%d BN=%d BK=%d | Thread tile: TM=%d TN=%d\n", I8_BM, I8_BN, I8_BK, I8_TM, I8_TN);
+    std::fprintf(g_manifest, "i8consts k14 %d %d %d %d %d %d\n", I8_BM, I8_BN, I8_BK, I8_TM, I8_TN, I8_NTHREADS);
     // tests/test_int8_gemm.cu:97-101
     const int gemm_shapes[][3] = {{256, 256, 256}, {512, 512, 512}, {1024, 1024, 1024}, {2048, 2048, 2048},
                                   {512, 1024, 256}};
@@ -257,6 +293,9 @@ int main(int argc, char** argv) {
                                   {1, 8, 8, 1024}, {1, 16, 4, 256}, {8, 32, 8, 1024}};
     for (const auto& s : attn_shapes) attn_case(s[0], s[1], s[2], s[3], 64, 16);
     support_cases();
+    // tests/test_layernorm.cu:87-91
+    const int ln_shapes[][2] = {{1, 768}, {128, 768}, {1, 256}, {64, 768}, {512, 768}};
+    for (const auto& s : ln_shapes) layernorm_residual_case(s[0], s[1]);
     std::fclose(g_manifest);
     std::printf("compat_dropin: done\n");
     return 0;

@@ -16,7 +16,7 @@ COMPAT = os.path.join(ROOT, "include", "ie_compat.h")
 LIB = os.path.join(PKG, "libie_amd.so")
 
 
-SIGS_EXPECTED = 22  # entry points declared in include/ie_amd.h
+SIGS_EXPECTED = 23  # entry points declared in include/ie_amd.h
 
 
 def declared_c_functions(path=HDR):
@@ -166,6 +166,10 @@ def test_other_validation(ie):
     assert st(ie, "ie_kv_cache_write", n, FAKE, FAKE, FAKE, 0, FAKE, 1, 0, 12, 64, 16, n) == ie.IE_ERR_INVALID
     assert st(ie, "ie_kv_cache_append_batch", 2, FAKE, FAKE, FAKE, FAKE, 0, FAKE, 0, FAKE, 12, 64, 16, n) == ie.IE_ERR_INVALID
     assert st(ie, "ie_layernorm", 1, 0, FAKE, FAKE, FAKE, FAKE, 1e-5, n) == ie.IE_ERR_INVALID
+    assert st(ie, "ie_layernorm_residual", 1, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1e-5, n) == ie.IE_ERR_INVALID
+    assert st(ie, "ie_layernorm_residual", -1, 8, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1e-5, n) == ie.IE_ERR_INVALID
+    assert st(ie, "ie_layernorm_residual", 2, 8, FAKE, n, FAKE, FAKE, FAKE, FAKE, 1e-5, n) == ie.IE_ERR_INVALID
+    assert st(ie, "ie_layernorm_residual", 0, 8, n, n, n, n, n, n, 1e-5, n) == ie.IE_OK
     assert st(ie, "ie_vocab_proj", 17, FAKE, FAKE, FAKE, 768, 10, n) == ie.IE_ERR_INVALID
     assert st(ie, "ie_vocab_proj", 1, FAKE, FAKE, FAKE, 766, 10, n) == ie.IE_ERR_INVALID
     assert st(ie, "ie_argmax", 1, FAKE, 0, FAKE, n) == ie.IE_ERR_INVALID

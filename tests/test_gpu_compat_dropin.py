@@ -8,7 +8,8 @@ It restates tests/test_int8_gemm.cu:15-94 (srand(42) inputs, quantize A and
 B^T, run_int8_gemm; the reference's bound max |INT8 - FP32| < 0.012 sqrt(K))
 and tests/test_decode_attention.cu:48-140 (srand(42) Q/K/V, identity-table
 paged cache, max |diff| < 1e-5), and calls run_int8_gemm_bias /
-_bias_gelu / _bias_residual, run_layernorm, run_embedding,
+_bias_gelu / _bias_residual, run_layernorm, run_layernorm_residual (on
+tests/test_layernorm.cu's own cases), run_embedding,
 run_flash_attn_v2, sample_argmax and sample_top_k.  Here each output is
 checked against the oracle on the program's own inputs: quantizer, int32-exact
 GEMMs and embedding bit-exact, GELU 2e-6 relative plus the tanhf bound
@@ -119,6 +120,39 @@ def test_layernorm_in_place_and_embedding(orc, run_dir):
     want = orc.embedding(load(d, cs, "ids", np.int32), start, load(d, cs, "wte", np.float32, (V, dm)),
                          load(d, cs, "wpe", np.float32, (S, dm)))
     assert np.array_equal(load(d, cs, "out", np.float32, (seq, dm)), want)
+
+
+def test_k14_tile_constants(run_dir):
+    """I8_BM ... I8_NTHREADS (kernels/quantization/14_int8_gemm.cuh:11-16) as
+    the reference's INT8 bench prints them: the program compiles against the
+    drop-in header and sees the reference's values."""
+    (_, _, *vals), = cases_of(run_dir, "i8consts")
+    assert list(map(int, vals)) == [64, 64, 16, 4, 4, 256]
+
+
+def test_layernorm_residual_reference_cases(orc, run_dir):
+    """tests/test_layernorm.cu:34-91 through run_layernorm_residual: the
+    program's srand(42) inputs are the reference test's draws; residual_out
+    bit-exact (x + residual), out within 1e-5 of the output scale of the
+    oracle and within the reference's own 2e-4; in place gives the same bits."""
+    from test_oracle_attn_support import LN_REF_CASES, ln_reference_inputs
+
+    d = run_dir[0]
+    cases = cases_of(run_dir, "lnres")
+    assert [(int(r), int(c)) for _, _, r, c in cases] == LN_REF_CASES
+    for _, cs, rows, cols in cases:
+        rows, cols = int(rows), int(cols)
+        x, res, gamma, beta = (load(d, cs, n, np.float32) for n in ("x", "res", "gamma", "beta"))
+        rx, rres, rg, rb = ln_reference_inputs(orc, rows, cols)
+        assert np.array_equal(x, rx.ravel()) and np.array_equal(res, rres.ravel())
+        assert np.array_equal(gamma, rg) and np.array_equal(beta, rb)
+        want, want_res = orc.layernorm_residual(rx, rres, rg, rb)
+        out = load(d, cs, "out", np.float32, (rows, cols))
+        assert np.array_equal(load(d, cs, "res_out", np.float32, (rows, cols)), want_res), cs
+        assert np.abs(out - want).max() <= 1e-5 * np.abs(want).max(), cs
+        assert np.abs(out - want).max() < 2e-4, cs
+        assert np.array_equal(load(d, cs, "out_inplace", np.float32, (rows, cols)), out), cs
+        assert np.array_equal(load(d, cs, "res_out_inplace", np.float32, (rows, cols)), want_res), cs
 
 
 def test_flash_attn_v2(run_dir):

@@ -248,6 +248,24 @@ def test_edges(ie, orc):
     assert np.all(got == 0)
 
 
+@pytest.mark.parametrize("d,G,kv_dtype", [(64, 1, 0), (128, 4, 0), (128, 4, 1), (128, 8, 0)])
+def test_empty_table_rows(ie, d, G, kv_dtype):
+    """max_context_len 0 with num_blocks_per_seq 0: a table of zero columns.
+    No walk may read a table entry (every row is empty); the output is 0."""
+    import torch
+
+    B, H_kv = 5, 2
+    H_q = H_kv * G
+    Q = dev(rng(9).standard_normal((B, H_q, d)).astype(np.float32))
+    cache = torch.zeros(16 * H_kv * d, dtype=torch.float32, device="cuda")  # one block, never read
+    table = torch.zeros((B, 1), dtype=torch.int32, device="cuda")[:, :0]  # non-null pointer, zero columns
+    lens = torch.zeros(B, dtype=torch.int32, device="cuda")
+    for splits in (0, 1, 7):
+        out = torch.full_like(Q, float("nan"))
+        ie.decode_attn(Q, cache, cache, table, lens, 0, 16, H_kv, kv_dtype=kv_dtype, splits=splits, out=out)
+        assert np.all(host(out) == 0)
+
+
 def test_placement_invariance_bit_identical(ie):
     B, H_q, H_kv, d = 3, 16, 4, 128
     lens = np.array([900, 321, 1024])

@@ -15,6 +15,11 @@
 * Closed forms on the engine itself, GPT-2 Small shape: all linear weights
   zero -> logits = LN_f(wte[t] + wpe[p]) wte^T; weights zero, biases random ->
   x_L = x_0 + sum_l (out_bias_l + down_bias_l); LayerNorm gamma/beta random.
+* The same op-by-op check at BASELINE configs[4]'s context: a 128-token
+  prompt through the prefill path (all rows of every op), decode steps at
+  positions 128-131, 255 and 380-383 with the context between advanced by
+  prefill chunks, at batch 2 and 16; every composed result equal to the
+  engine's prefill and decode steps (unfused and fused) bit for bit.
 * BASELINE configs[4] at its stated length (prompt 128, 256 greedy tokens,
   batch 1 and 16): determinism, batch-16 rows equal to batch-1 runs, the
   fused step equal to the unfused one, graph replay equal to eager.
@@ -128,6 +133,76 @@ class CAbiStep:
             assert np.array_equal(g, want), ("gemm", epi, np.abs(g - want).max())
         return got
 
+    def prefill(self, tokens, check=True):
+        """A prompt chunk of P tokens per sequence at positions pos .. pos + P - 1
+        (GPT2Engine::Impl::prefill: M = B x P rows per op, the K/V of the chunk
+        appended, causal prefill attention over the cache; the reference's
+        is_prefill branch, src/gpt2_engine.cu:447-528 and :660-676).  Every op
+        is checked on all its rows against the oracle on its device input
+        (check=False runs the same ops unchecked, to advance the context);
+        returns the last token's logits [B, V]."""
+        ie, orc, torch = self.ie, self.orc, self.torch
+        tokens = np.asarray(tokens, np.int32)
+        B, P = tokens.shape
+        assert B == self.B
+        d, H, dh, start, M = self.d, self.H, self.dh, self.pos, B * P
+        ids = torch.from_numpy(tokens.reshape(-1).copy()).cuda()
+        x = torch.empty((M, d), device="cuda")
+        for b in range(B):
+            ie.embedding(ids[b * P:(b + 1) * P], start, self.g["wte"], self.g["wpe"], out=x[b * P:(b + 1) * P])
+        if check:
+            want = np.concatenate([orc.embedding(tokens[b], start, self.h["wte"], self.h["wpe"]) for b in range(B)])
+            assert np.array_equal(x.cpu().numpy(), want), "embedding"
+        pos_bt = start + np.arange(P)
+        lens = np.tile(pos_bt + 1, B).astype(np.int32)   # query (b, t) sees start + t + 1 tokens
+        table_rep = np.repeat(self.table_h, P, axis=0)
+        saved = (self._ln, self._quant, self._gemm)
+        if not check:
+            self._ln = lambda x_, g, b_, gh, bh: ie.layernorm(x_, g, b_)
+            self._quant = lambda x_: ie.quantize(x_)
+            self._gemm = lambda q_, s_, w, wh, epi, residual=None, out=None: ie.int8_gemm(
+                q_, w[0], s_, w[1], epi, w[2], residual, out=out)
+        try:
+            for l, (L, Lh) in enumerate(zip(self.layers, self.layers_h)):
+                xn = self._ln(x, L["ln1_gamma"], L["ln1_beta"], Lh["ln1_gamma"], Lh["ln1_beta"])
+                q8, s8 = self._quant(xn)
+                qkv = self._gemm(q8, s8, L["qkv"], Lh["qkv"], ie.EPI_BIAS)
+                q = qkv[:, :d].contiguous().view(B, P, H, dh)
+                k = qkv[:, d:2 * d].contiguous().view(B, P, H, dh)
+                v = qkv[:, 2 * d:].contiguous().view(B, P, H, dh)
+                for b in range(B):
+                    ie.kv_cache_write(k[b], v[b], self.kc[l], self.vc[l], self.table[b], start, BLOCK)
+                attn = ie.prefill_attn(q, self.kc[l], self.vc[l], self.table, start, BLOCK, H).view(M, d)
+                if check:
+                    kc_h, vc_h = self.kc[l].cpu().numpy(), self.vc[l].cpu().numpy()
+                    slots = self.table_h[:, pos_bt // BLOCK]                      # [B, P]
+                    assert np.array_equal(kc_h[slots, pos_bt % BLOCK], k.cpu().numpy()), "kv write"
+                    assert np.array_equal(vc_h[slots, pos_bt % BLOCK], v.cpu().numpy()), "kv write"
+                    want = orc.decode_attn(q.cpu().numpy().reshape(M, H, dh), kc_h, vc_h, table_rep, lens,
+                                           start + P, BLOCK, H).reshape(M, d)
+                    err = _rel(attn.cpu().numpy(), want)
+                    self._note("prefill_attn", err)
+                    assert err <= 1e-5, ("prefill_attn", l, err)
+                q8, s8 = self._quant(attn)
+                self._gemm(q8, s8, L["out"], Lh["out"], ie.EPI_BIAS_RESIDUAL, residual=x, out=x)
+                xn = self._ln(x, L["ln2_gamma"], L["ln2_beta"], Lh["ln2_gamma"], Lh["ln2_beta"])
+                q8, s8 = self._quant(xn)
+                hdn = self._gemm(q8, s8, L["ffn_up"], Lh["ffn_up"], ie.EPI_BIAS_GELU)
+                q8, s8 = self._quant(hdn)
+                self._gemm(q8, s8, L["ffn_down"], Lh["ffn_down"], ie.EPI_BIAS_RESIDUAL, residual=x, out=x)
+        finally:
+            self._ln, self._quant, self._gemm = saved
+        last = x.view(B, P, d)[:, P - 1].contiguous()
+        xf = self._ln(last, self.g["lnf_g"], self.g["lnf_b"], self.h["lnf_g"], self.h["lnf_b"])
+        logits = ie.vocab_proj(xf, self.g["wte"]).cpu().numpy()
+        want = np.stack([orc.vocab_proj(row, self.h["wte"]) for row in xf.cpu().numpy()])
+        err = _rel(logits, want)
+        self._note("lm_head", err)
+        assert err <= 1e-5, ("lm_head", err)
+        self.pos = start + P
+        self.positions.fill_(self.pos)
+        return logits
+
     def step(self, tokens):
         ie, orc, torch = self.ie, self.orc, self.torch
         B, d, H, dh = self.B, self.d, self.H, self.dh
@@ -198,6 +273,60 @@ def test_teacher_forced_gpt2_small_every_op(ie, orc, small_dir):
     print("worst relative error per op:", cabi.worst)
     unfused.close()
     fused.close()
+
+
+# BASELINE configs[4]'s context: a 128-token prompt prefilled, then decode
+# steps at positions 128-131 (the first block after the prompt), 255 (the last
+# slot of block 15) and 380-383 (the run's last positions), the context
+# between them advanced by prefill chunks continuing the session.
+CFG5_SCHEDULE = [("prefill", 128, True), ("decode", 4), ("prefill", 123, True), ("decode", 1),
+                 ("prefill", 124, True), ("decode", 4)]
+
+
+def run_schedule(ie, orc, small_dir, B, schedule, seed):
+    """Drive the op-by-op C ABI model and the engine (unfused and fused)
+    through the same prompt chunks and decode tokens; every composed result
+    must equal the engines' bit for bit."""
+    rng = np.random.default_rng(seed)
+    cabi = CAbiStep(ie, orc, str(small_dir), B)
+    engines = [ie.Engine(small_dir, max_batch=B, fuse=False), ie.Engine(small_dir, max_batch=B)]
+    try:
+        for item in schedule:
+            if item[0] == "prefill":
+                _, P, check = item
+                toks = rng.integers(0, GPT2_SMALL["vocab_size"], (B, P)).astype(np.int32)
+                want = cabi.prefill(toks, check=check)
+                for e in engines:
+                    assert np.array_equal(e.prefill(toks), want), ("prefill", cabi.pos)
+            else:
+                for _ in range(item[1]):
+                    at = cabi.pos
+                    t = rng.integers(0, GPT2_SMALL["vocab_size"], B).astype(np.int32)
+                    want = cabi.step(t)
+                    for e in engines:
+                        assert np.array_equal(e.step(t), want), ("decode", at)
+        assert cabi.pos == 128 + 255 and all(e.session_tokens() == cabi.pos for e in engines)
+    finally:
+        for e in engines:
+            e.close()
+    print("worst relative error per op:", cabi.worst)
+
+
+def test_teacher_forced_cfg5_context_batch2(ie, orc, small_dir):
+    """GPT-2 Small at BASELINE configs[4]'s context, batch 2: the prompt's
+    prefill and every decode step checked op by op on all rows."""
+    run_schedule(ie, orc, small_dir, 2, CFG5_SCHEDULE, 23)
+
+
+def test_teacher_forced_cfg5_context_batch16(ie, orc, small_dir):
+    """The same at batch 16 (the configs[4] batch): the 128-token prompt
+    (2048 rows per op) and every decode step checked on all rows; the two
+    chunks that advance the context between the decode positions run the
+    same ops unchecked (checked at batch 2 above) and still must equal the
+    engines' prefill bit for bit."""
+    sched = [("prefill", 128, True), ("decode", 4), ("prefill", 123, False), ("decode", 1),
+             ("prefill", 124, False), ("decode", 4)]
+    run_schedule(ie, orc, small_dir, 16, sched, 29)
 
 
 def closed_form_logits(t, tokens, pos):

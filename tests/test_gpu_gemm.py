@@ -339,6 +339,80 @@ def test_8192_cube_sampled_rows_and_checksum(ie, orc):
     assert np.array_equal(C[torch.from_numpy(rows).cuda()].cpu().numpy(), want)
 
 
+def test_headline_8192_cube_plain_as_timed(ie, orc):
+    """The timed headline itself: bench.headline_inputs (N(0,1) from seed 42,
+    quantized per row by the library) and bench_headline's call, Plain
+    epilogue, into one C.  That is gemm_i8_256_kernel<Plain, 8 waves, buffer
+    copies>: 1024 tiles walked 4 per persistent workgroup, 64 K stages.
+    Checked three ways:
+      * rows on both edges of every 256-row tile and columns on both edges of
+        every 256-column tile, bit-exact against the oracle's Plain GEMM
+        (the reference's ((float)acc * sA) * sB, 14_int8_gemm.cu:154);
+      * the whole matrix bit-exact against the int32 path's accumulators
+        dequantized with the same two fp32 roundings (torch, elementwise),
+        the int32 matrix itself held by exact int64 row and column checksums;
+      * a second launch into the same C gives the same bits."""
+    import torch
+
+    import bench
+
+    M = N = K = 8192
+    Ap, Bp, sA, sB = bench.headline_inputs(ie)
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ie.int8_gemm(Ap, Bp, sA, sB, ie.EPI_PLAIN, out=C)  # bench_headline's launch
+    torch.cuda.synchronize()
+    first = C.clone()
+    ie.int8_gemm(Ap, Bp, sA, sB, ie.EPI_PLAIN, out=C)
+    torch.cuda.synchronize()
+    assert torch.equal(C, first)
+    del first
+
+    edges = np.unique(np.concatenate([np.arange(0, M, 256), np.arange(255, M, 256), [4100]]))
+    idx = torch.from_numpy(edges).cuda()
+    Bp_h, sB_h, sA_h = Bp.cpu().numpy(), sB.cpu().numpy(), sA.cpu().numpy()
+    want_rows = orc.gemm(Ap[idx].cpu().numpy(), Bp_h, sA_h[edges], sB_h, 0)
+    assert np.array_equal(C[idx].cpu().numpy(), want_rows)
+    want_cols = orc.gemm(Ap.cpu().numpy(), Bp_h[edges], sA_h, sB_h[edges], 0)
+    assert np.array_equal(C[:, idx].cpu().numpy(), want_cols)
+
+    acc = ie.int8_gemm(Ap, Bp, epilogue=ie.EPI_I32, path=ie.PATH_MFMA)
+    torch.cuda.synchronize()
+    A8 = Ap.view(torch.int8).view(M, K)
+    B8 = Bp.view(torch.int8).view(N, K)
+    colsum = A8.to(torch.int64).sum(0).cpu().numpy()
+    rowsum = B8.to(torch.int64).sum(0).cpu().numpy()
+    assert np.array_equal(acc.to(torch.int64).sum(0).cpu().numpy(), B8.cpu().numpy().astype(np.int64) @ colsum)
+    assert np.array_equal(acc.to(torch.int64).sum(1).cpu().numpy(), A8.cpu().numpy().astype(np.int64) @ rowsum)
+    deq = (acc.to(torch.float32) * sA[:, None]) * sB[None, :]
+    assert torch.equal(C, deq)
+
+
+@pytest.mark.parametrize("M,N", [(4352, 4352), (4300, 4350)])
+@pytest.mark.parametrize("epi", [0, 1, 3])
+def test_big_tile_persistent_odd_stages(ie, orc, epi, M, N):
+    """Plain / Bias / Residual on the 256x256-tile kernel with more tiles than
+    CUs (17 x 17 = 289: persistent workgroups take a second tile) and an odd
+    number of 128-byte K stages (K = 640: 5), so a second tile's first stage
+    lands in the other LDS slot; rows from both edges of every 256-row tile,
+    bit-exact against the oracle."""
+    K = 640
+    A, W = problem(M, N, K, 70 + epi)
+    r = rng(71)
+    bias = r.standard_normal(N).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi, dev(bias) if epi else None,
+                            dev(res) if epi == 3 else None, path=ie.PATH_MFMA))
+    rows = sorted(set(range(0, M, 256)) | set(range(255, M, 256)) | {M - 2, M - 1})
+    want = orc.gemm(Ap[rows], Wp, sA[rows], sW, epi, bias if epi else None, res[rows] if epi == 3 else None)
+    assert np.array_equal(got[rows], want)
+    cols = sorted(set(range(0, N, 256)) | set(range(255, N, 256)) | {N - 1})
+    want_c = orc.gemm(Ap, Wp[cols], sA, sW[cols], epi, bias[cols] if epi else None,
+                      res[:, cols] if epi == 3 else None)
+    assert np.array_equal(got[:, cols], want_c)
+
+
 @pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
 def test_cfg2_m512_lm_head_shape_full(ie, orc, epi):
     """M = 512 activations x the 768 x 50257 LM-head

@@ -89,6 +89,36 @@ def test_layernorm(ie, orc, rows, cols):
     assert np.array_equal(host(xd), got)
 
 
+@pytest.mark.parametrize("rows,cols", [(1, 768), (128, 768), (5, 256), (3, 767), (64, 3072)])
+def test_layernorm_residual(ie, orc, rows, cols):
+    """ie_layernorm_residual (run_layernorm_residual): residual_out = x + res
+    bit-exact, out within 1e-5 of the output scale of the oracle and equal bit
+    for bit to ie_layernorm of residual_out; the same results with out and
+    residual_out aliased to the inputs (cols 767: the scalar path)."""
+    r = rng(rows * 7 + cols)
+    x = (r.standard_normal((rows, cols)) * 2).astype(np.float32)
+    res = (r.standard_normal((rows, cols)) + 0.5).astype(np.float32)
+    g = (1 + 0.2 * r.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * r.standard_normal(cols)).astype(np.float32)
+    want, want_res = orc.layernorm_residual(x, res, g, b)
+    gd, bd = dev(g), dev(b)
+    out, res_out = ie.layernorm_residual(dev(x), dev(res), gd, bd)
+    got, got_res = host(out), host(res_out)
+    assert np.array_equal(got_res, want_res)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    assert np.array_equal(host(ie.layernorm(res_out, gd, bd)), got)
+    for alias in ("out=x,res_out=res", "out=res,res_out=x", "both=x"):
+        xd, rd = dev(x), dev(res)
+        o, ro = {"out=x,res_out=res": (xd, rd), "out=res,res_out=x": (rd, xd), "both=x": (xd, xd)}[alias]
+        if alias == "both=x":
+            scratch_out, _ = ie.layernorm_residual(xd, rd, gd, bd, out=xd, residual_out=xd)
+            # out written over residual_out: only out survives
+            assert np.array_equal(host(scratch_out), got), alias
+            continue
+        ie.layernorm_residual(xd, rd, gd, bd, out=o, residual_out=ro)
+        assert np.array_equal(host(o), got) and np.array_equal(host(ro), got_res), alias
+
+
 def test_embedding_vocab_argmax(ie, orc):
     import torch
 

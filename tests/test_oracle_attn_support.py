@@ -184,6 +184,55 @@ def test_layernorm_vs_torch(orc):
     assert np.abs(got - want).max() < 1e-5
 
 
+LN_REF_CASES = [(1, 768), (128, 768), (1, 256), (64, 768), (512, 768)]  # tests/test_layernorm.cu:87-91
+
+
+def ln_reference_inputs(orc, rows, cols):
+    """tests/test_layernorm.cu:36-42: srand(42); x, residual as
+    rand()/RAND_MAX*2-1; gamma = 0.8 + rand()/RAND_MAX*0.4; beta =
+    rand()/RAND_MAX*0.2 - 0.1 (float arithmetic, RAND_MAX converted to
+    float)."""
+    g = orc.GlibcRand(42)
+    x = g.uniform(rows * cols).reshape(rows, cols)
+    res = g.uniform(rows * cols).reshape(rows, cols)
+    f = np.float32
+    unit = lambda: f(g.next()) / f(2147483647)  # noqa: E731
+    gamma = np.array([f(0.8) + unit() * f(0.4) for _ in range(cols)], np.float32)
+    beta = np.array([unit() * f(0.2) - f(0.1) for _ in range(cols)], np.float32)
+    return x, res, gamma, beta
+
+
+def test_layernorm_residual_vs_torch(orc):
+    """residual_out is the fp32 sum x + residual exactly; out is torch's
+    float64 layer_norm of that sum; neither LN(x) + residual nor LN(residual)
+    passes; and on the reference test's own srand(42) inputs the reference's
+    bound (2e-4 absolute) holds against its own two-pass CPU formula
+    (tests/test_layernorm.cu:13-31) evaluated in float64."""
+    import torch
+
+    r = rng(5)
+    x = (r.standard_normal((6, 768)) * 2).astype(np.float32)
+    res = (r.standard_normal((6, 768)) + 1).astype(np.float32)
+    g = r.standard_normal(768).astype(np.float32)
+    b = r.standard_normal(768).astype(np.float32)
+    out, res_out = orc.layernorm_residual(x, res, g, b)
+    assert np.array_equal(res_out, np.add(x, res, dtype=np.float32))
+    want = torch.nn.functional.layer_norm(torch.from_numpy(res_out).double(), (768,), torch.from_numpy(g).double(),
+                                          torch.from_numpy(b).double(), eps=1e-5).numpy()
+    assert np.abs(out - want).max() < 1e-5
+    assert np.abs(out - (orc.layernorm(x, g, b) + res)).max() > 0.1
+    assert np.abs(out - orc.layernorm(res, g, b)).max() > 0.1
+    for rows, cols in LN_REF_CASES:
+        x, res, gamma, beta = ln_reference_inputs(orc, rows, cols)
+        assert ((gamma >= 0.8) & (gamma <= 1.2)).all() and (np.abs(beta) <= 0.1).all()
+        out, res_out = orc.layernorm_residual(x, res, gamma, beta)
+        y = x.astype(np.float64) + res
+        mean = y.mean(axis=1, keepdims=True)
+        var = ((y - mean) ** 2).mean(axis=1, keepdims=True)
+        ref = gamma * (y - mean) / np.sqrt(var + 1e-5) + beta
+        assert np.abs(out - ref).max() < 2e-4 and np.abs(res_out - y).max() < 2e-4, (rows, cols)
+
+
 def test_embedding_vocab_argmax(orc):
     r = rng(6)
     V, d, L = 50, 16, 20
