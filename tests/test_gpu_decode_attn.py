@@ -258,11 +258,15 @@ def test_empty_table_rows(ie, d, G, kv_dtype):
     H_q = H_kv * G
     Q = dev(rng(9).standard_normal((B, H_q, d)).astype(np.float32))
     cache = torch.zeros(16 * H_kv * d, dtype=torch.float32, device="cuda")  # one block, never read
-    table = torch.zeros((B, 1), dtype=torch.int32, device="cuda")[:, :0]  # non-null pointer, zero columns
+    table = torch.zeros(1, dtype=torch.int32, device="cuda")  # a real pointer; the rows have 0 columns
     lens = torch.zeros(B, dtype=torch.int32, device="cuda")
     for splits in (0, 1, 7):
         out = torch.full_like(Q, float("nan"))
-        ie.decode_attn(Q, cache, cache, table, lens, 0, 16, H_kv, kv_dtype=kv_dtype, splits=splits, out=out)
+        S = ie.num_splits(0, 16, splits)
+        ws = torch.empty(ie.workspace_bytes(B, H_q, d, S) // 4, device="cuda")
+        P = ie._ptr
+        ie.check("ie_decode_attn", B, H_q, H_kv, d, P(Q), P(cache), P(cache), kv_dtype, P(table), P(lens), 0, 16,
+                 0, P(out), P(ws), ws.numel() * 4, splits, ie._stream())
         assert np.all(host(out) == 0)
 
 
