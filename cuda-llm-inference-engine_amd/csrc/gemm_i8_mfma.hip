@@ -163,6 +163,10 @@ void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s) {
         launch_gemm_i8_generic(a, s);
         return;
     }
+    if (gemm_i8_wide_applies(a)) {
+        launch_gemm_i8_wide(a, s);
+        return;
+    }
     if (gemm_i8_big_applies(a)) {
         launch_gemm_i8_big(a, s);
         return;

@@ -87,6 +87,9 @@ void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s);
 // 256x256-tile MFMA GEMM for large M, N (gemm_i8_mfma256.hip).
 bool gemm_i8_big_applies(const GemmArgs& a);
 void launch_gemm_i8_big(const GemmArgs& a, hipStream_t s);
+// Write-dominated shapes (K == 768, M <= 1024, wide N; gemm_i8_wide.hip).
+bool gemm_i8_wide_applies(const GemmArgs& a);
+void launch_gemm_i8_wide(const GemmArgs& a, hipStream_t s);
 // LDS-tiled MFMA GEMM for prefill-sized problems (gemm_i8_tile.hip): tile
 // shape BM * 1000 + BN chosen for a problem, applicability, launch.
 int gemm_i8_tile_shape(const GemmArgs& a);

@@ -438,6 +438,42 @@ def test_cfg2_m512_lm_head_shape_full(ie, orc, epi):
         assert np.array_equal(got, want), np.abs(got - want).max()
 
 
+# ------------------------------------------------------------------ wide (write-dominated) kernel
+@pytest.mark.parametrize("M,N", [(17, 50000), (300, 50001), (700, 20000), (1024, 12800), (512, 49153)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
+def test_wide_kernel_shapes(ie, orc, epi, M, N):
+    """Shapes the write-dominated kernel takes (K = 768, M <= 1024, wide N):
+    one to four 256-row panels (700 rows: three panels on a 240-workgroup
+    grid), ragged panels and column chunks, M = 17 (one row past the GEMV
+    range); rows from both edges of every 32-row block and every panel, all
+    columns; int32 and Plain / Bias / Residual bit-exact, GELU 2e-6.  The
+    residual epilogue writes in place over the residual, as the engine calls
+    it."""
+    K = 768
+    A, W = problem(M, N, K, 90 + epi + M)
+    r = rng(91 + N)
+    bias = r.standard_normal(N).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    rows = sorted({m for b in range(0, M, 32) for m in (b, b + 31) if m < M} | {M - 1})
+    if epi == 4:
+        got = host(ie.int8_gemm(dev(Ap), dev(Wp), epilogue=ie.EPI_I32))
+        assert np.array_equal(got[rows], orc.gemm_i32(Ap[rows], Wp))
+        return
+    out = dev(res) if epi == 3 else None
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi, dev(bias) if epi else None, out, out=out))
+    want = orc.gemm(Ap[rows], Wp, sA[rows], sW, epi, bias if epi else None, res[rows] if epi == 3 else None)
+    if epi == 2:
+        # device vs glibc tanhf: 2e-6 relative plus 1.2e-7 |v| (v = the
+        # BiasOnly value), the bound of the drop-in test's GELU check
+        v = orc.gemm(Ap[rows], Wp, sA[rows], sW, 1, bias)
+        err = np.abs(got[rows].astype(np.float64) - want)
+        assert (err <= 2e-6 * np.abs(want) + 1.2e-7 * np.abs(v)).all(), err.max()
+    else:
+        assert np.array_equal(got[rows], want), np.abs(got[rows] - want).max()
+
+
 # ------------------------------------------------------------------ 256x256 tiles
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (3000, 5000, 512), (2304, 8192, 768),
                                    (8192, 3000, 256), (4096, 8448, 384), (4352, 4352, 640)])
