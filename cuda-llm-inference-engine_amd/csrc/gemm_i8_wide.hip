@@ -30,11 +30,15 @@
 //     one chunk stream sit on the same XCD (workgroup id mod 8) and walk the
 //     same chunks at the same pace, so the second panel's copy of a chunk is
 //     an L2 hit; with P panels a weight byte leaves HBM once and enters P CUs.
+//   * the A panel (8 blocks of 32 rows x 768 bytes, one per wave) arrives
+//     through LDS: a block has a B chunk's shape and layout, so it is copied
+//     with the same coalesced 1 KiB LDS-direct wave-loads (6 blocks, then the
+//     last 2 beside the first B chunks) and each wave reads its operands from
+//     there; loaded straight into registers (each wave instruction 32 rows x
+//     32 bytes) the panel cost 4.5-6 us of a 34 us launch;
 //   * the int32 K-sum is exact in any order, so each workgroup walks K in its
-//     own rotated order (k-step s covers K bytes 32 ((s + rot) mod 24) ..):
-//     the 128 workgroups that load the same A panel at start then request
-//     different lines at any moment instead of the same one (in one order,
-//     the panel loads cost 4.5-7 us of a 34.5 us launch);
+//     own rotated order (k-step s covers K bytes 32 ((s + rot) mod 24) ..),
+//     which spreads the workgroups' simultaneous requests for one panel;
 // LDS layout of a chunk: row r (weight row, C column) holds its 48 16-byte
 // pieces with piece t at slot t ^ (r & 7), so the 8 lanes of a fragment read
 // group hit 8 different bank groups.
@@ -56,7 +60,8 @@ constexpr int PIECES = KW / 16;      // 16-byte pieces per weight row (48)
 constexpr int PANEL = 256;           // A rows per workgroup
 constexpr int CN = 32;               // C columns per chunk
 constexpr int CHUNK = CN * KW;       // bytes of one B chunk (24 KiB)
-constexpr int RING = 4;              // chunks in LDS (96 KiB), RING - 1 in flight
+constexpr int RING = 4;              // B chunks in the ring, RING - 1 in flight
+constexpr int SLOTS = 6;             // 24 KiB LDS slots: the B ring, and the A panel's first 6 blocks at start
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
@@ -67,15 +72,18 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
                                                               const float* __restrict__ sA,
                                                               const float* __restrict__ sB, const float* bias,
                                                               const float* residual, void* C, int panels) {
-    // the B ring, then per slot the chunk's 32 column scales and 32 biases
-    __shared__ __attribute__((aligned(1024))) int8_t lds[RING * CHUNK + RING * 256];
-    float (*cols)[64] = reinterpret_cast<float (*)[64]>(lds + RING * CHUNK);
+    // SLOTS chunk slots (the B ring uses RING of them), then per ring slot
+    // the chunk's 32 column scales and 32 biases
+    __shared__ __attribute__((aligned(1024))) int8_t lds[SLOTS * CHUNK + RING * 256];
+    float (*cols)[64] = reinterpret_cast<float (*)[64]>(lds + SLOTS * CHUNK);
     constexpr bool HAS_SCALE = EPI != IE_EPI_I32;
     constexpr bool HAS_BIAS = EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL;
     constexpr bool HAS_RES = EPI == IE_EPI_BIAS_RESIDUAL;
     constexpr int RB = PANEL / 32 / NW;           // 32-row blocks per wave
     constexpr int WLOADS = CHUNK / 1024 / NW;     // wave-loads of 1 KiB per wave per chunk
     static_assert(RB * NW * 32 == PANEL && WLOADS * NW * 1024 == CHUNK, "panel and chunk split over waves");
+    static_assert(RB == 1 && SLOTS >= RING && SLOTS < NW && 2 * SLOTS - NW >= RING - 1,
+                  "A blocks 0..SLOTS-1 in round one, the rest in slots clear of B chunks 0..RING-2");
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -124,13 +132,30 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
     const int rot = (stream * 7 + panel * 13) % KS;
     auto kk = [&](int s) { const int t = s + rot; return t < KS ? t : t - KS; };
     const int mrow0 = panel * PANEL + wave * 32 * RB;
+    // A block b (rows panel * PANEL + 32 b ..) into LDS slot `slot`, in the
+    // B chunk layout; `nb` blocks copied by all waves together, wave-load
+    // jl of the set covering 1 KiB of block jl / 24
+    auto issue_a = [&](int b0, int slot0, int nb) {
+        const int per = nb * (CHUNK / 1024) / NW;
+#pragma unroll
+        for (int u = 0; u < per; ++u) {
+            const int jl = wave * per + u;
+            const int blk = jl / (CHUNK / 1024), jb = jl % (CHUNK / 1024);
+            const int q = jb * 64 + lane;
+            const int r = q / PIECES, t = q % PIECES;
+            const int row = min(panel * PANEL + (b0 + blk) * 32 + r, M - 1);
+            const int8_t* src = A + (size_t)row * KW + ((t ^ (r & 7)) << 4);
+            __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(lds + (slot0 + blk) * CHUNK + jb * 1024), 16, 0,
+                                             0);
+        }
+    };
+    // the wave's operands from its block in LDS (same reads as a B fragment)
     i32x4 a[RB][KS];
+    auto read_a = [&](int slot) {
+        const int8_t* al = lds + slot * CHUNK + fr * KW;
 #pragma unroll
-    for (int i = 0; i < RB; ++i) {
-        const int8_t* ar = A + (size_t)min(mrow0 + i * 32 + fr, M - 1) * KW + 16 * h;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) a[i][s] = *reinterpret_cast<const i32x4*>(ar + 32 * kk(s));
-    }
+        for (int s = 0; s < KS; ++s) a[0][s] = *reinterpret_cast<const i32x4*>(al + (((2 * kk(s) + h) ^ (fr & 7)) << 4));
+    };
     // Lane (fr, h) of a 32 x 32 accumulator block holds rows 8 q + 4 h + r
     // (v = 4 q + r) of column fr.
     auto mrow = [&](int i, int v) { return mrow0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3); };
@@ -142,26 +167,36 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
             for (int v = 0; v < 16; ++v) sa[i][v] = sA[min(mrow(i, v), M - 1)];
     }
 
-    // Prologue: chunks 0 .. RING - 2 copied, A and its scales in registers,
-    // all landed before the loop (so the loop's first waits need no count of
-    // their own).
-#pragma unroll
-    for (int p = 0; p < RING - 1; ++p) issue(p, p);
-#pragma unroll
-    for (int i = 0; i < RB; ++i)
-#pragma unroll
-        for (int s = 0; s < KS; ++s) asm volatile("" ::"v"(a[i][s]));
+    // Prologue.  Round one: A blocks 0 .. SLOTS - 1 into slots 0 .. SLOTS - 1;
+    // their waves read them.  Round two: the last NW - SLOTS blocks into the
+    // top slots and B chunks 0 .. RING - 2 into the ring slots; the last
+    // waves read their blocks while the chunks are in flight.  The row
+    // scales were requested first, so they have landed with round one.
+    issue_a(0, 0, SLOTS);
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) asm volatile("" ::"v"(sa[i][v]));
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (wave < SLOTS) read_a(wave);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    issue_a(SLOTS, SLOTS - (NW - SLOTS), NW - SLOTS);
+#pragma unroll
+    for (int p = 0; p < RING - 1; ++p) issue(p, p);
+    constexpr int COPIES = WLOADS + (HAS_SCALE ? 1 : 0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((RING - 1) * COPIES) : "memory");
+    __builtin_amdgcn_s_barrier();
+    if (wave >= SLOTS) read_a(wave - (NW - SLOTS));  // blocks SLOTS.. sit in slots 2 SLOTS - NW ..
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
     // Vector-memory operations a wave issues per chunk: its copies, the
     // residual gathers and the C stores (vmcnt counts stores).  Waiting at
     // chunk j (j >= RING - 1) finds the stores and gathers of chunk
-    // j - RING + 1 and RING - 2 whole chunks issued after chunk j's copies.
-    constexpr int COPIES = WLOADS + (HAS_SCALE ? 1 : 0);
+    // j - RING + 1 and RING - 2 whole chunks issued after chunk j's copies;
+    // the first RING - 1 chunks were issued in the prologue, so fewer
+    // operations follow them.
     constexpr int GATHER = HAS_RES ? 16 * RB : 0;
     constexpr int STORES = 16 * RB;
     constexpr int AFTER = GATHER + STORES + (RING - 2) * (COPIES + GATHER + STORES);
@@ -169,6 +204,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
     // (and at most the next chunk's copies), which have had a chunk's time
     constexpr int WAITN = AFTER < 63 ? AFTER : 63;
     static_assert(AFTER >= WAITN, "the wait covers chunk j's copies");
+    constexpr int ITER = COPIES + GATHER + STORES;
+    constexpr int W0 = (RING - 2) * COPIES;
+    constexpr int W1 = (RING - 3) * COPIES + ITER;
+    constexpr int W2 = 2 * ITER < 63 ? 2 * ITER : 63;
+    static_assert(RING == 4, "W0..W2 cover the prologue's chunks");
 
     for (int j = 0; j < mine; ++j) {
         const int c = stream + j * streams;
@@ -177,7 +217,14 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
         // the barrier also means every wave is done reading chunk j - 1, whose
         // slot the copies issued next refill
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
+        if (j >= RING - 1)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
+        else if (j == 0)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W0) : "memory");
+        else if (j == 1)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W1) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W2) : "memory");
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         issue(j + RING - 1, (j + RING - 1) % RING);
