@@ -253,8 +253,13 @@ def bench_gemm512(ie):
         C = torch.empty((M, N), dtype=torch.float32, device="cuda")
         ms = graph_time(lambda i: ie.int8_gemm(A, B, sA, sB, ie.EPI_PLAIN, out=C), 20)
         tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-        out.append({"M": M, "K": K, "N": N, "us": round(ms * 1e3, 2), "TOPs": round(tops, 1)})
-        log(f"gemm M=512 K={K} N={N}: {ms * 1e3:.2f} us {tops:.1f} TOP/s")
+        byt = gemm_bytes(M, N, K)
+        # arithmetic intensity 2MNK / bytes is below the 629 op/B ridge for
+        # every shape here: HBM is the bound
+        out.append({"M": M, "K": K, "N": N, "us": round(ms * 1e3, 2), "TOPs": round(tops, 1),
+                    "bytes": byt, "GBps": round(byt / (ms * 1e-3) / 1e9, 1),
+                    "frac_hbm": round(byt / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3), "bound": "hbm"})
+        log(f"gemm M=512 K={K} N={N}: {ms * 1e3:.2f} us {tops:.1f} TOP/s {out[-1]['frac_hbm']} of HBM")
     return out
 
 
@@ -507,6 +512,7 @@ CALIB_BYTES = 1 << 30
 TRAFFIC_GEMV = [("gemv_8192_m1", 1, 8192, 8192), ("gemv_8192_m16", 16, 8192, 8192),
                 ("gemv_head_m1", 1, 768, 50257), ("gemv_head_m16", 16, 768, 50257),
                 ("gemv_28672_m1", 1, 8192, 28672)]
+TRAFFIC_M512 = (512, 768, 50257)  # (M, K, N), label gemm_m512_head
 
 
 def pmc_child(ie):
@@ -536,6 +542,13 @@ def pmc_child(ie):
         torch.cuda.synchronize()
         del W
     attn_case(ie, 32, 32, 8, 128, 8192, False, False, 8192, max_copies=1)
+    torch.cuda.synchronize()
+    # cfg2's M = 512 x 768 x 50257 GEMM (the write-dominated kernel), fresh C
+    M, K, N = TRAFFIC_M512
+    A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
+    W = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g).view(torch.int32)
+    C = torch.empty((M, N), device="cuda")
+    ie.int8_gemm(A, W, torch.ones(M, device="cuda"), torch.ones(N, device="cuda"), ie.EPI_PLAIN, out=C)
     torch.cuda.synchronize()
 
 
@@ -595,6 +608,8 @@ def measure_traffic():
                 gemv_i += 1
             elif "decode_attn_balanced_kernel" in name:
                 vals["attn"] = v
+            elif "gemm_i8_wide_kernel" in name:
+                vals["gemm_m512_head"] = v
         if "gemm" in vals:
             vals["gemm"] = sum(vals["gemm"]) / len(vals["gemm"])
         for k, v in vals.items():
@@ -608,6 +623,7 @@ def measure_traffic():
                            "write_factor": round(w_scale, 4)}}
     alg = {lbl: gemm_bytes(M, N, K) for lbl, M, K, N in TRAFFIC_GEMV}
     alg["gemm"] = gemm_bytes(8192, 8192, 8192)
+    alg["gemm_m512_head"] = gemm_bytes(TRAFFIC_M512[0], TRAFFIC_M512[2], TRAFFIC_M512[1])
     for k, v in out.items():
         if k != "copy" and "FETCH_SIZE" in v and "WRITE_SIZE" in v:
             fb, wb = int(v["FETCH_SIZE"] * f_scale), int(v["WRITE_SIZE"] * w_scale)
