@@ -55,7 +55,7 @@ __device__ __forceinline__ i32x4 read_frag(const int8_t* lds_oper, int row, int 
     return *reinterpret_cast<const i32x4*>(lds_oper + row * BK + ((chunk ^ swz(row)) << 4));
 }
 
-template <int EPI, int BM, int BN, int NSTAGE>
+template <int EPI, int BM, int BN, int NSTAGE, bool NT>
 __global__ __launch_bounds__(256) void gemm_i8_tile_kernel(int M, int N, int K, const int8_t* __restrict__ A,
                                                            const int8_t* __restrict__ BT,
                                                            const float* __restrict__ sA,
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void gemm_i8_tile_kernel(int M, int N, int K, 
             for (int j = 0; j < NJ; ++j) {
                 const int n = cbase + j * 32;
                 if (n < N)
-                    store_epilogue_v<EPI>(C, (size_t)m * N + n, acc[i][j][v], sa[i][v], sb[j], bv[j], rv[i][v][j]);
+                    store_epilogue_v<EPI, NT>(C, (size_t)m * N + n, acc[i][j][v], sa[i][v], sb[j], bv[j], rv[i][v][j]);
             }
         }
     }
@@ -230,9 +230,13 @@ struct TileLaunch {
     template <int BM, int BN, int NSTAGE>
     static void go(const GemmArgs& a, hipStream_t s) {
         const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
-        gemm_i8_tile_kernel<EPI, BM, BN, NSTAGE><<<tm * tn, 256, 0, s>>>(
-            a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB,
-            a.bias, a.residual, a.C, tm, tn);
+        // C of 16 MiB or more goes out with non-temporal stores (M = 2048:
+        // N = 2304 12.5 -> 10.9 us, N = 3072 13.5 -> 11.0 us; at N = 768,
+        // 6.3 MB of C, they measured slower: 6.15 -> 6.7 us)
+        auto* k = (size_t)a.M * a.N * 4 >= ((size_t)16 << 20) ? gemm_i8_tile_kernel<EPI, BM, BN, NSTAGE, true>
+                                                            : gemm_i8_tile_kernel<EPI, BM, BN, NSTAGE, false>;
+        k<<<tm * tn, 256, 0, s>>>(a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A),
+                                 reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C, tm, tn);
     }
     // Measured on the GPT-2 prefill shapes (M = 128-2048, K = 768 / 3072,
     // N = 768-3072, bias epilogue; same box, bit-identical C): two stages
