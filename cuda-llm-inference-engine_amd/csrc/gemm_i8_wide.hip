@@ -31,11 +31,12 @@
 //     same chunks at the same pace, so the second panel's copy of a chunk is
 //     an L2 hit; with P panels a weight byte leaves HBM once and enters P CUs.
 //   * the A panel (8 blocks of 32 rows x 768 bytes, one per wave) arrives
-//     through LDS: a block has a B chunk's shape and layout, so it is copied
-//     with the same coalesced 1 KiB LDS-direct wave-loads (6 blocks, then the
-//     last 2 beside the first B chunks) and each wave reads its operands from
-//     there; loaded straight into registers (each wave instruction 32 rows x
-//     32 bytes) the panel cost 4.5-6 us of a 34 us launch;
+//     mostly through LDS: a block has a B chunk's shape and layout, so blocks
+//     0-5 are copied with the same coalesced 1 KiB LDS-direct wave-loads and
+//     their waves read their operands from there, while waves 6 and 7 load
+//     theirs straight into registers at the same time (each wave instruction
+//     32 rows x 32 bytes: the whole panel that way cost 4.5-6 us of a 34 us
+//     launch; a second LDS round for blocks 6-7 was one more round trip);
 //   * the int32 K-sum is exact in any order, so each workgroup walks K in its
 //     own rotated order (k-step s covers K bytes 32 ((s + rot) mod 24) ..),
 //     which spreads the workgroups' simultaneous requests for one panel;
@@ -82,8 +83,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
     constexpr int RB = PANEL / 32 / NW;           // 32-row blocks per wave
     constexpr int WLOADS = CHUNK / 1024 / NW;     // wave-loads of 1 KiB per wave per chunk
     static_assert(RB * NW * 32 == PANEL && WLOADS * NW * 1024 == CHUNK, "panel and chunk split over waves");
-    static_assert(RB == 1 && SLOTS >= RING && SLOTS < NW && 2 * SLOTS - NW >= RING - 1,
-                  "A blocks 0..SLOTS-1 in round one, the rest in slots clear of B chunks 0..RING-2");
+    static_assert(RB == 1 && SLOTS >= RING && SLOTS < NW, "A blocks 0..SLOTS-1 through LDS, the rest direct");
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -167,11 +167,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
             for (int v = 0; v < 16; ++v) sa[i][v] = sA[min(mrow(i, v), M - 1)];
     }
 
-    // Prologue.  Round one: A blocks 0 .. SLOTS - 1 into slots 0 .. SLOTS - 1;
-    // their waves read them.  Round two: the last NW - SLOTS blocks into the
-    // top slots and B chunks 0 .. RING - 2 into the ring slots; the last
-    // waves read their blocks while the chunks are in flight.  The row
-    // scales were requested first, so they have landed with round one.
+    // Prologue: waves SLOTS.. load their A block into registers while all
+    // waves copy blocks 0 .. SLOTS - 1 into slots 0 .. SLOTS - 1 (and the row
+    // scales were requested before both); once everything has landed the
+    // first waves read their blocks, and after that B chunks 0 .. RING - 2 go
+    // into the ring slots.
+    if (wave >= SLOTS) {
+        const int8_t* ar = A + (size_t)min(mrow0 + fr, M - 1) * KW + 16 * h;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) a[0][s] = *reinterpret_cast<const i32x4*>(ar + 32 * kk(s));
+    }
     issue_a(0, 0, SLOTS);
 #pragma unroll
     for (int i = 0; i < RB; ++i)
@@ -181,15 +186,14 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
     __builtin_amdgcn_s_barrier();
     if (wave < SLOTS) read_a(wave);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // every operand register is final here (the compiler's own waits, if
+    // any, stay out of the loop)
+#pragma unroll
+    for (int s = 0; s < KS; ++s) asm volatile("" ::"v"(a[0][s]));
     __builtin_amdgcn_s_barrier();
-    issue_a(SLOTS, SLOTS - (NW - SLOTS), NW - SLOTS);
 #pragma unroll
     for (int p = 0; p < RING - 1; ++p) issue(p, p);
     constexpr int COPIES = WLOADS + (HAS_SCALE ? 1 : 0);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((RING - 1) * COPIES) : "memory");
-    __builtin_amdgcn_s_barrier();
-    if (wave >= SLOTS) read_a(wave - (NW - SLOTS));  // blocks SLOTS.. sit in slots 2 SLOTS - NW ..
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
     // Vector-memory operations a wave issues per chunk: its copies, the
     // residual gathers and the C stores (vmcnt counts stores).  Waiting at
