@@ -83,12 +83,37 @@ def test_i32_mfma_exact(ie, orc, M, K, N):
     i32_case(ie, orc, M, N, K, ie.PATH_MFMA, M * 11 + N + K)
 
 
-@pytest.mark.parametrize("M", [1, 3, 4, 5, 8, 16])
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 8, 9, 13, 16])
 def test_i32_lm_head_shape(ie, orc, M):
     """The 768 x 50257 LM head (N % 4 == 1: a partial last 4-feature item):
     the burst GEMV for M <= 8 with one and two activation-row blocks, the
-    MFMA GEMV at M = 16."""
+    MFMA GEMV at M = 9-16 (a partial last 16-feature group)."""
     i32_case(ie, orc, M, 50257, 768, ie.PATH_AUTO, 99 + M)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 16390, 3072), (16, 16400, 3072), (12, 50257, 768), (16, 20001, 768)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
+def test_wide_n_mfma_gemv_epilogues(ie, orc, M, N, K, epi):
+    """The MFMA GEMV at 9 <= M <= 16 with a wide N (K = 768 / 3072): ragged
+    last 16-feature group, every epilogue; int32 and Plain/Bias/Residual
+    bit-exact, GELU to 2e-6."""
+    A, W = problem(M, N, K, 17 * M + N + epi)
+    r = rng(37 + epi)
+    bias = (r.standard_normal(N) * 0.5).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    if epi == 4:
+        got = host(ie.int8_gemm(dev(Ap), dev(Wp), epilogue=ie.EPI_I32, path=ie.PATH_GEMV))
+        assert np.array_equal(got, orc.gemm_i32(Ap, Wp))
+        return
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi, dev(bias) if epi else None,
+                            dev(res) if epi == 3 else None, path=ie.PATH_GEMV))
+    want = orc.gemm(Ap, Wp, sA, sW, epi, bias if epi else None, res if epi == 3 else None)
+    if epi == 2:
+        assert np.allclose(got, want, rtol=2e-6, atol=1e-7), np.abs(got - want).max()
+    else:
+        assert np.array_equal(got, want), np.abs(got - want).max()
 
 
 @pytest.mark.parametrize("M,N", [(2, 16390), (7, 16387)])
