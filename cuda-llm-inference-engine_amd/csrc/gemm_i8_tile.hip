@@ -9,7 +9,7 @@
 // small workgroups per CU cover it better than one large one.  The tile is
 // BM x BN (64 x 64 or 128 x 64) on four waves (2 x 2, each (BM/2) x (BN/2)
 // as 32x32 blocks of v_mfma_i32_32x32x32_i8), and K advances through a ring
-// of NSTAGE 128-byte stages in LDS (2, or 4 for long K), NSTAGE - 1 of them
+// of NSTAGE 128-byte stages in LDS (2-3, or 4 for long K), NSTAGE - 1 of them
 // in flight while one is read:
 //   * global -> LDS copies are global_load_lds_dwordx4 (16 B per lane straight
 //     into LDS); a wave-load fills 8 rows x 128 B; the lane -> global address
@@ -239,11 +239,16 @@ struct TileLaunch {
                                  reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C, tm, tn);
     }
     // Measured on the GPT-2 prefill shapes (M = 128-2048, K = 768 / 3072,
-    // N = 768-3072, bias epilogue; same box, bit-identical C): two stages
-    // (more workgroups per CU: 48-64 KiB of LDS each) beat three and four
-    // except over long K (K = 3072: four); 128 x 64 tiles beat 64 x 64 once
-    // there are two per CU (M = 2048, N = 2304: 12.1 against 13.7 us);
-    // 128 x 128 tiles lost everywhere (one workgroup per CU).
+    // N = 768-3072, bias epilogue; same box, bit-identical C): 128 x 64 tiles
+    // beat 64 x 64 once there are two per CU (M = 2048, N = 2304: 12.1
+    // against 13.7 us) and keep two stages (three: 11.1 -> 13.7 us, fewer
+    // workgroups per CU); 64 x 64 tiles take three stages at K = 768, two in
+    // flight, which pays when the weights come from the MALL or HBM rather
+    // than L2 (GPT-2 prefill TTFT at batch 1: 0.705 -> 0.684 ms; weights
+    // rotated through 1 GiB, M = 512, N = 768: 7.55 -> 5.95 us; the same
+    // weights every launch, L2-resident: 5.09 -> 5.20 us), and four over long
+    // K (K = 3072); a whole-K ring (six stages, one workgroup per CU) lost
+    // wherever there are more tiles than CUs; 128 x 128 tiles lost everywhere.
     static void run(const GemmArgs& a, hipStream_t s) {
         const bool long_k = a.K >= 2048;
         if (gemm_i8_tile_shape(a) == 128064) {
@@ -251,7 +256,7 @@ struct TileLaunch {
             else go<128, 64, 2>(a, s);
         } else {
             if (long_k) go<64, 64, 4>(a, s);
-            else go<64, 64, 2>(a, s);
+            else go<64, 64, 3>(a, s);
         }
     }
 };
