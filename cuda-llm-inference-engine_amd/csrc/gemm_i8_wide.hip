@@ -67,6 +67,25 @@ constexpr int SLOTS = 6;             // 24 KiB LDS slots: the B ring, and the A 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
 
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N < 63 ? N : 63) : "memory");
+}
+
+// The wait for chunk j < RING - 1, issued in the prologue back to back: after
+// its copies come those of chunks j + 1 .. RING - 2 and j whole iterations
+// (ITER operations each) of the loop.
+template <int J, int COPIES, int ITER>
+__device__ __forceinline__ void wait_prologue_chunk(int j) {
+    if constexpr (J < RING - 1) {
+        if (j == J) {
+            wait_vm<(RING - 2 - J) * COPIES + J * ITER>();
+            return;
+        }
+        wait_prologue_chunk<J + 1, COPIES, ITER>(j);
+    }
+}
+
 template <int EPI, bool NT, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, const int8_t* __restrict__ A,
                                                               const int8_t* __restrict__ BT,
@@ -209,10 +228,6 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
     constexpr int WAITN = AFTER < 63 ? AFTER : 63;
     static_assert(AFTER >= WAITN, "the wait covers chunk j's copies");
     constexpr int ITER = COPIES + GATHER + STORES;
-    constexpr int W0 = (RING - 2) * COPIES;
-    constexpr int W1 = (RING - 3) * COPIES + ITER;
-    constexpr int W2 = 2 * ITER < 63 ? 2 * ITER : 63;
-    static_assert(RING == 4, "W0..W2 cover the prologue's chunks");
 
     for (int j = 0; j < mine; ++j) {
         const int c = stream + j * streams;
@@ -222,13 +237,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
         // slot the copies issued next refill
         __builtin_amdgcn_sched_barrier(0);
         if (j >= RING - 1)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
-        else if (j == 0)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W0) : "memory");
-        else if (j == 1)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W1) : "memory");
+            wait_vm<WAITN>();
         else
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W2) : "memory");
+            wait_prologue_chunk<0, COPIES, ITER>(j);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         issue(j + RING - 1, (j + RING - 1) % RING);

@@ -251,11 +251,38 @@ def test_register_streamed_kernel(ie, orc, M, N, K, epi):
 @pytest.mark.parametrize("epi", [0, 2, 3, 4])
 def test_prefill_sized_wide_gemm(ie, orc, M, N, K, epi):
     """A batch of prompts through the QKV / FFN-up projections: the LDS tile
-    kernel with 128x64 tiles (2048x2304, two per CU) and 64x64 tiles
-    (1100x2100), two-stage ring; ragged M and N, int32 and Plain/Residual
-    bit-exact, GELU to 2e-6."""
+    kernel with 128x64 tiles (2048x2304, two per CU, two-stage ring) and 64x64
+    tiles (1100x2100, three-stage ring); ragged M and N, int32 and
+    Plain/Residual bit-exact, GELU to 2e-6."""
     A, W = problem(M, N, K, 3 * M + N + epi)
     r = rng(17 + epi)
+    bias = (r.standard_normal(N) * 0.5).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    if epi == 4:
+        got = host(ie.int8_gemm(dev(Ap), dev(Wp), epilogue=ie.EPI_I32, path=ie.PATH_MFMA))
+        assert np.array_equal(got, orc.gemm_i32(Ap, Wp))
+        return
+    got = host(ie.int8_gemm(dev(Ap), dev(Wp), dev(sA), dev(sW), epi,
+                            dev(bias) if epi else None, dev(res) if epi == 3 else None, path=ie.PATH_MFMA))
+    want = orc.gemm(Ap, Wp, sA, sW, epi, bias if epi else None, res if epi == 3 else None)
+    if epi == 2:
+        assert np.allclose(got, want, rtol=2e-6, atol=1e-7), np.abs(got - want).max()
+    else:
+        assert np.array_equal(got, want), np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("M,N,K", [(600, 1100, 128), (600, 1000, 384), (700, 900, 640)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
+def test_tile_kernel_short_k_ring(ie, orc, M, N, K, epi):
+    """The 64x64 LDS tile kernel's three-stage ring against K stage counts
+    below, equal to and past the ring: one 128-byte stage (the prologue and
+    the loop re-read it into the other slots), three, and five (the ring
+    wraps: the last stage sits in slot 1); ragged M and N, the whole output, int32 and
+    Plain/Bias/Residual bit-exact, GELU to 2e-6."""
+    A, W = problem(M, N, K, 13 * M + N + K + epi)
+    r = rng(29 + epi)
     bias = (r.standard_normal(N) * 0.5).astype(np.float32)
     res = r.standard_normal((M, N)).astype(np.float32)
     Ap, sA = orc.quantize(A)
