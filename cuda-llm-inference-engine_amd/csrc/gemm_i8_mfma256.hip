@@ -92,6 +92,31 @@ __device__ __forceinline__ i32x4 read_frag(const int8_t* lds_oper, int row, int 
     return *reinterpret_cast<const i32x4*>(lds_oper + row * BK + ((chunk ^ swz(row)) << 4));
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 4 x 4 transpose inside each lane quad: on entry lane j of the quad holds
+// element (r, j) in x[r], on return element (j, c) in x[c].  Two butterfly
+// rounds, each trading one bit of the lane index for one bit of the register
+// index through a DPP quad permutation (quad_perm [1, 0, 3, 2], then
+// [2, 3, 0, 1]).
+__device__ __forceinline__ void quad_transpose(int32_t (&x)[4], int j) {
+    const bool b0 = j & 1, b1 = j & 2;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {  // lane bit 0 <-> register bit 0: registers 2s, 2s + 1
+        const int32_t send = b0 ? x[2 * s] : x[2 * s + 1];
+        const int32_t recv = __builtin_amdgcn_update_dpp(0, send, 0xB1, 0xf, 0xf, false);
+        x[2 * s] = b0 ? recv : x[2 * s];
+        x[2 * s + 1] = b0 ? x[2 * s + 1] : recv;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {  // lane bit 1 <-> register bit 1: registers s, s + 2
+        const int32_t send = b1 ? x[s] : x[s + 2];
+        const int32_t recv = __builtin_amdgcn_update_dpp(0, send, 0x4E, 0xf, 0xf, false);
+        x[s] = b1 ? recv : x[s];
+        x[s + 2] = b1 ? x[s + 2] : recv;
+    }
+}
+
 // NW = 4: 2 x 2 waves of 128 x 128 (one wave per SIMD); NW = 8: 2 x 4 waves
 // of 128 x 64 (two per SIMD, so one wave's MFMAs can run while the other
 // waits at the stage barrier or for its copies).
@@ -135,6 +160,19 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     i32x16 acc[4][NJ];
 
     const int nk = K / BK;
+    constexpr bool HAS_BIAS = EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL;
+    constexpr bool HAS_RES = EPI == IE_EPI_BIAS_RESIDUAL;
+    // Full tiles of a C with 16-byte rows (N % 4 == 0) leave through the
+    // quad-transposed epilogue below, except with a residual (its 128 loads
+    // per lane would not stay in registers).
+    const bool quad_c = !HAS_RES && (N & 3) == 0 && ((uintptr_t)C & 15) == 0;
+    // Vector-memory operations a full tile's epilogue issues at least: the
+    // quad path's scale and bias loads and 16-byte stores, the per-element
+    // path's 16 * 4 * NJ stores.  The next tile's stage-1 copies come just
+    // before them, so its first wait lets this many stay in flight.
+    constexpr int EPI_OPS = HAS_RES ? 16 * 4 * NJ
+                                    : (EPI != IE_EPI_I32 ? (HAS_BIAS ? 8 : 4) * NJ + 16 : 0) + 16 * NJ;
+    constexpr int W_EARLY = EPI_OPS < 63 ? EPI_OPS : 63;
     // Copies stage kt_src of the tile at (m0_, n0_) into LDS slot `slot`.
     // Every iteration issues one stage, so the loop body is branch-free: the
     // last stage's iteration issues the next tile's stage 0, or, after the
@@ -221,9 +259,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     // stage), otherwise this tile's stage kt + 1; EARLY (stage 0 of every
     // tile after the first): stage 1 was issued by the previous tile's last
     // stage, ahead of that tile's C stores, so this stage issues nothing and,
-    // when every lane of the previous tile stored all its values (full_prev:
-    // at least 63 vector-memory operations follow those copies), its wait
-    // lets 63 of them stay in flight instead of draining the stores.  The
+    // when the previous tile was full (full_prev: its epilogue issued at
+    // least EPI_OPS vector-memory operations after those copies), its wait
+    // lets W_EARLY of them stay in flight instead of draining the stores.  The
     // last stage is peeled so every stage's body stays one basic block, with
     // the copies interleaved among its MFMAs.
     auto stage = [&](int kt, auto next_c, auto early_c, bool full_prev) {
@@ -263,7 +301,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
                 mfma_rows(slot, 0, 2);
                 __builtin_amdgcn_sched_barrier(0);
                 if (EARLY && full_prev)
-                    asm volatile("s_waitcnt vmcnt(63) lgkmcnt(0)" ::: "memory");
+                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(W_EARLY) : "memory");
                 else
                     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_STAGE) : "memory");
                 __builtin_amdgcn_s_barrier();
@@ -296,71 +334,117 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     stage(nk - 1, std::true_type{}, std::false_type{}, false);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 
-    // Epilogue.  Lane l of a 32x32 block holds rows 8q + 4(l/32) + r (q, r < 4)
-    // of column l % 32.  Every operand the stores of a 32-row block need
-    // (scales, bias, residual; clamped indices) is gathered before its first
-    // store and consumed once in straight-line code: loaded inside the branchy
-    // store loop, each would wait for all earlier stores (vmcnt counts stores,
-    // and C may alias them).  Two waves per SIMD leave no room for all 64 row
-    // scales beside the accumulators, so they are gathered one block at a time.
-    // C goes out as non-temporal stores (2316 against 2187 TOP/s at 8192^3
-    // with the stores cached in L2; 16-byte stores of quad-transposed values
-    // measured no faster).
+    // Full tiles with 16-byte C rows: the accumulators are transposed inside
+    // each lane quad (quad_transpose), so lane j of a quad holds row 8q +
+    // 4(l/32) + j of the quad's four consecutive columns and C leaves in
+    // 16-byte non-temporal stores, 32 per lane instead of 128; a row then
+    // needs one row scale per four values, so all of the tile's 16 row
+    // scales, its column scales and biases are requested before the first
+    // store, and no load waits behind the stores.  The per-element arithmetic
+    // is epilogue_value's, as in the path below, so C has the same bits.
     const int h = lane >> 5;
     const int rbase = m0 + wm * 128 + 4 * h;
-    const int cbase = n0 + wn * 32 * NJ + (lane & 31);
-    constexpr bool HAS_BIAS = EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL;
-    constexpr bool HAS_RES = EPI == IE_EPI_BIAS_RESIDUAL;
-    float sb[NJ] = {}, bv[NJ] = {};
-    if constexpr (EPI != IE_EPI_I32) {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int n = min(cbase + j * 32, N - 1);
-            sb[j] = sB[n];
-            if constexpr (HAS_BIAS) bv[j] = bias[n];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float sa[16] = {}, rv[16][NJ] = {};
+    if (quad_c && m0 + BM <= M && n0 + BN <= N) {
+        const int jq = lane & 3;
+        const int qcol = n0 + wn * 32 * NJ + (lane & 28);  // the quad's first column (block j = 0)
+        float sb4[NJ][4] = {}, bv4[NJ][4] = {}, sa1[4][4] = {};
         if constexpr (EPI != IE_EPI_I32) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = min(rbase + i * 32 + 8 * (v >> 2) + (v & 3), M - 1);
-                sa[v] = sA[m];
-                if constexpr (HAS_RES) {
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                    for (int j = 0; j < NJ; ++j) rv[v][j] = residual[(size_t)m * N + min(cbase + j * 32, N - 1)];
+                for (int c = 0; c < 4; ++c) {
+                    sb4[j][c] = sB[qcol + 32 * j + c];
+                    if constexpr (HAS_BIAS) bv4[j][c] = bias[qcol + 32 * j + c];
+                }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sa1[i][q] = sA[rbase + i * 32 + 8 * q + jq];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    int32_t x[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                    acc[i][j][4 * q + 3]};
+                    quad_transpose(x, jq);
+                    const size_t idx = (size_t)(rbase + i * 32 + 8 * q + jq) * N + qcol + 32 * j;
+                    if constexpr (EPI == IE_EPI_I32) {
+                        const i32x4 o = {x[0], x[1], x[2], x[3]};
+                        __builtin_nontemporal_store(o, reinterpret_cast<i32x4*>(static_cast<int32_t*>(C) + idx));
+                    } else {
+                        f32x4 o;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            o[c] = epilogue_value<EPI>(x[c], sa1[i][q], sb4[j][c], bv4[j][c], 0.0f);
+                        __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(static_cast<float*>(C) + idx));
+                    }
+                }
+    } else {
+        // Partial tiles, other C widths and the residual epilogue: one store per
+        // value.  Lane l of a 32x32 block holds rows 8q + 4(l/32) + r (q, r < 4)
+        // of column l % 32.  Every operand the stores of a 32-row block need
+        // (scales, bias, residual; clamped indices) is gathered before its
+        // first store and consumed once in straight-line code: loaded inside
+        // the branchy store loop, each would wait for all earlier stores
+        // (vmcnt counts stores, and C may alias them).  Two waves per SIMD
+        // leave no room for all 64 row scales beside the accumulators, so they
+        // are gathered one block at a time.  C goes out as non-temporal stores
+        // (2316 against 2187 TOP/s at 8192^3 with the stores cached in L2).
+        const int cbase = n0 + wn * 32 * NJ + (lane & 31);
+        float sb[NJ] = {}, bv[NJ] = {};
+        if constexpr (EPI != IE_EPI_I32) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int n = min(cbase + j * 32, N - 1);
+                sb[j] = sB[n];
+                if constexpr (HAS_BIAS) bv[j] = bias[n];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sa[16] = {}, rv[16][NJ] = {};
+            if constexpr (EPI != IE_EPI_I32) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int m = min(rbase + i * 32 + 8 * (v >> 2) + (v & 3), M - 1);
+                    sa[v] = sA[m];
+                    if constexpr (HAS_RES) {
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j) rv[v][j] = residual[(size_t)m * N + min(cbase + j * 32, N - 1)];
+                    }
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    asm volatile("" ::"v"(sa[v]));
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        if constexpr (HAS_RES) asm volatile("" ::"v"(rv[v][j]));
+                }
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    asm volatile("" ::"v"(sb[j]));
+                    if constexpr (HAS_BIAS) asm volatile("" ::"v"(bv[j]));
                 }
             }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                asm volatile("" ::"v"(sa[v]));
+                const int m = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
+                if (m >= M) continue;
 #pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    if constexpr (HAS_RES) asm volatile("" ::"v"(rv[v][j]));
-            }
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                asm volatile("" ::"v"(sb[j]));
-                if constexpr (HAS_BIAS) asm volatile("" ::"v"(bv[j]));
-            }
-        }
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int m = rbase + i * 32 + 8 * (v >> 2) + (v & 3);
-            if (m >= M) continue;
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int n = cbase + j * 32;
-                if (n < N)
-                    store_epilogue_v<EPI, true>(C, (size_t)m * N + n, acc[i][j][v], sa[v], sb[j], bv[j], rv[v][j]);
+                for (int j = 0; j < NJ; ++j) {
+                    const int n = cbase + j * 32;
+                    if (n < N)
+                        store_epilogue_v<EPI, true>(C, (size_t)m * N + n, acc[i][j][v], sa[v], sb[j], bv[j], rv[v][j]);
+                }
             }
         }
     }
     if (!more) break;
-    // a full tile: every lane stored all its 16 * 4 * NJ values, so at
-    // least 63 vector-memory operations follow the next tile's stage-1 copies
+    // a full tile: its epilogue issued at least EPI_OPS vector-memory
+    // operations after the next tile's stage-1 copies
     prev_full = m0 + BM <= M && n0 + BN <= N;
     first_tile = false;
     // the next tile: its stage 0 has landed and its first fragments are loaded

@@ -551,6 +551,32 @@ def test_big_tile_kernel_exact(ie, orc, M, N, K):
     assert np.array_equal(C[idx].cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("epi", [0, 4])
+def test_big_tile_c_not_16_byte_aligned(ie, orc, epi):
+    """N % 4 == 0 but C 4 bytes past a 16-byte boundary: the 256x256-tile
+    kernel keeps the per-element stores (the quad-transposed 16-byte stores
+    need aligned rows), same bits as an aligned C and the oracle."""
+    import torch
+
+    M, N, K = 2304, 4096, 768  # 9 x 16 tiles of 256 x 256
+    A, W = problem(M, N, K, 60 + epi)
+    Ap, sA = orc.quantize(A)
+    Wp, sW = orc.quantize(W)
+    dt = torch.int32 if epi == 4 else torch.float32
+    buf = torch.zeros(M * N + 4, dtype=dt, device="cuda")
+    C_off = buf[1:1 + M * N].view(M, N)
+    assert C_off.data_ptr() % 16 == 4
+    args = (dev(Ap), dev(Wp), dev(sA), dev(sW), epi) if epi != 4 else (dev(Ap), dev(Wp), None, None, epi)
+    got = host(ie.int8_gemm(*args, out=C_off, path=ie.PATH_MFMA))
+    aligned = host(ie.int8_gemm(*args, path=ie.PATH_MFMA))
+    assert np.array_equal(got.view(np.int32), aligned.view(np.int32))
+    rows = [0, 1, 255, 256, 1000, M - 1]
+    if epi == 4:
+        assert np.array_equal(got[rows], orc.gemm_i32(Ap[rows], Wp))
+    else:
+        assert np.array_equal(got[rows], orc.gemm(Ap[rows], Wp, sA[rows], sW, 0))
+
+
 @pytest.mark.parametrize("M,N", [(2304, 4100), (2300, 4100), (2300, 4099)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 def test_big_tile_epilogues(ie, orc, epi, M, N):
