@@ -166,13 +166,6 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     // quad-transposed epilogue below, except with a residual (its 128 loads
     // per lane would not stay in registers).
     const bool quad_c = !HAS_RES && (N & 3) == 0 && ((uintptr_t)C & 15) == 0;
-    // Vector-memory operations a full tile's epilogue issues at least: the
-    // quad path's scale and bias loads and 16-byte stores, the per-element
-    // path's 16 * 4 * NJ stores.  The next tile's stage-1 copies come just
-    // before them, so its first wait lets this many stay in flight.
-    constexpr int EPI_OPS = HAS_RES ? 16 * 4 * NJ
-                                    : (EPI != IE_EPI_I32 ? (HAS_BIAS ? 8 : 4) * NJ + 16 : 0) + 16 * NJ;
-    constexpr int W_EARLY = EPI_OPS < 63 ? EPI_OPS : 63;
     // Copies stage kt_src of the tile at (m0_, n0_) into LDS slot `slot`.
     // Every iteration issues one stage, so the loop body is branch-free: the
     // last stage's iteration issues the next tile's stage 0, or, after the
@@ -241,7 +234,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     constexpr int SUB = BK / 32;  // MFMA k-substeps per stage (even)
     static_assert(SUB % 2 == 0, "fragment slots alternate within a stage");
     int base = 0;  // LDS slot of the tile's stage 0 (stage kt sits in slot (kt + base) % 2)
-    bool first_tile = true, prev_full = false;
+    bool first_tile = true;
     for (;;) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -258,13 +251,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     // One K stage; NEXT: its copies are the next tile's stage 0 (the last
     // stage), otherwise this tile's stage kt + 1; EARLY (stage 0 of every
     // tile after the first): stage 1 was issued by the previous tile's last
-    // stage, ahead of that tile's C stores, so this stage issues nothing and,
-    // when the previous tile was full (full_prev: its epilogue issued at
-    // least EPI_OPS vector-memory operations after those copies), its wait
-    // lets W_EARLY of them stay in flight instead of draining the stores.  The
-    // last stage is peeled so every stage's body stays one basic block, with
-    // the copies interleaved among its MFMAs.
-    auto stage = [&](int kt, auto next_c, auto early_c, bool full_prev) {
+    // stage, ahead of that tile's C stores, and this wave's copies of it
+    // landed at the wait that ends that tile's K loop, so this stage issues
+    // nothing and its wait is for LDS reads only (the barrier covers the
+    // other waves' copies): the previous tile's stores stay in flight instead
+    // of being drained.  The last stage is peeled so every stage's body stays
+    // one basic block, with the copies interleaved among its MFMAs.
+    auto stage = [&](int kt, auto next_c, auto early_c) {
         constexpr bool NEXT = decltype(next_c)::value;
         constexpr bool EARLY = decltype(early_c)::value;
         const int8_t* sa = lds + ((kt + base) % NSTAGE) * STAGE;
@@ -300,8 +293,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
                 // slot, unused; otherwise the next tile's stage 0)
                 mfma_rows(slot, 0, 2);
                 __builtin_amdgcn_sched_barrier(0);
-                if (EARLY && full_prev)
-                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(W_EARLY) : "memory");
+                if constexpr (EARLY)
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 else
                     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * LOADS_PER_STAGE) : "memory");
                 __builtin_amdgcn_s_barrier();
@@ -327,11 +320,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
     };
     int kt0 = 0;
     if (!first_tile && nk >= 2) {
-        stage(0, std::false_type{}, std::true_type{}, prev_full);
+        stage(0, std::false_type{}, std::true_type{});
         kt0 = 1;
     }
-    for (int kt = kt0; kt + 1 < nk; ++kt) stage(kt, std::false_type{}, std::false_type{}, false);
-    stage(nk - 1, std::true_type{}, std::false_type{}, false);
+    for (int kt = kt0; kt + 1 < nk; ++kt) stage(kt, std::false_type{}, std::false_type{});
+    stage(nk - 1, std::true_type{}, std::false_type{});
+    // every copy this wave issued has landed, the next tile's stage 1 (issued
+    // by the last stage) included: the next tile's first stage relies on it
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 
     // Full tiles with 16-byte C rows: the accumulators are transposed inside
@@ -443,9 +438,6 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_256_kernel(
         }
     }
     if (!more) break;
-    // a full tile: its epilogue issued at least EPI_OPS vector-memory
-    // operations after the next tile's stage-1 copies
-    prev_full = m0 + BM <= M && n0 + BN <= N;
     first_tile = false;
     // the next tile: its stage 0 has landed and its first fragments are loaded
     T = Tn;
