@@ -228,6 +228,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
     constexpr int WAITN = AFTER < 63 ? AFTER : 63;
     static_assert(AFTER >= WAITN, "the wait covers chunk j's copies");
     constexpr int ITER = COPIES + GATHER + STORES;
+    // A store whose lanes all hold rows past M is branched around (no lane
+    // active), so only a wave whose 32 rows are all below M is sure to issue
+    // its STORES per chunk; the others count only their copies and gathers,
+    // which are unconditional.  (A chunk's first column is always below N,
+    // so a full-row wave issues every store.)
+    const bool rows_full = mrow0 + 32 * RB <= M;
+    constexpr int ITER_C = COPIES + GATHER;
+    constexpr int AFTER_C = GATHER + (RING - 2) * ITER_C;
+    constexpr int WAITN_C = AFTER_C < 63 ? AFTER_C : 63;
 
     for (int j = 0; j < mine; ++j) {
         const int c = stream + j * streams;
@@ -236,10 +245,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_wide_kernel(int M, int N, 
         // the barrier also means every wave is done reading chunk j - 1, whose
         // slot the copies issued next refill
         __builtin_amdgcn_sched_barrier(0);
-        if (j >= RING - 1)
-            wait_vm<WAITN>();
-        else
+        if (j >= RING - 1) {
+            if (rows_full)
+                wait_vm<WAITN>();
+            else
+                wait_vm<WAITN_C>();
+        } else if (rows_full) {
             wait_prologue_chunk<0, COPIES, ITER>(j);
+        } else {
+            wait_prologue_chunk<0, COPIES, ITER_C>(j);
+        }
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         issue(j + RING - 1, (j + RING - 1) % RING);
