@@ -814,8 +814,9 @@ void launch_slice(const GemmArgs& a, hipStream_t s) {
     // Plain loads: a wave instruction here reads 16 rows x 64 bytes, half of
     // each 128-byte line, a pattern that streams slower with non-temporal
     // loads (M = 8 / 16 at N = 8192: 0.58 / 0.556 -> 0.589 / 0.566 of HBM
-    // peak).  A ring of 2 sets of 8 loads: measured level with 4 sets.
-    auto* k = a.M <= 8 ? gemv_i8_slice_kernel<EPI, false, 2, 8> : gemv_i8_slice_kernel<EPI, false, 2>;
+    // peak).  A ring of 2 sets of 8 loads: measured level with 4 sets.  Only
+    // 9 <= M <= 16 come here (16 staged rows).
+    auto* k = gemv_i8_slice_kernel<EPI, false, 2>;
     k<<<blocks, 512, 0, s>>>(a.M, a.N, ks_log, reinterpret_cast<const int8_t*>(a.A),
                              reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C);
 }
@@ -883,14 +884,16 @@ void launch_mt(const GemmArgs& a, hipStream_t s) {
         if (a.K == 3072) return launch_mfma16<EPI, 48>(a, s);
     }
     // K = 8192 (measured at N = 8192 and 28672, M = 1..16, fraction of HBM
-    // peak on one box): the 4-feature-item kernel for M <= 4 (N = 28672:
+    // peak on one box): the 4-feature-item kernel for M <= 8 (N = 28672:
     // M = 1 0.76 -> 0.79 against dot4, M = 4 0.62 -> 0.79 against the 16-row
-    // MFMA kernels) and for any M once each wave has two items or more
-    // (N >= 16384; N = 28672, M = 16: 0.64 -> 0.69); below that the K-sliced
-    // 16-feature kernel, whose activation staging costs a quarter as much
-    // per wave (N = 8192, M = 16: 0.55 against 0.49).
+    // MFMA kernels; N = 8192, rotated weights: M = 5 / 8 13.94 / 14.31 ->
+    // 13.15 / 13.59 us against the K-sliced kernel) and for any M once each
+    // wave has two items or more (N >= 16384; N = 28672, M = 16: 0.64 ->
+    // 0.69); below that, at 9 <= M <= 16, the K-sliced 16-feature kernel,
+    // whose activation staging costs a quarter as much per wave (N = 8192,
+    // M = 16: 14.9 against 16.9 us).
     if (a.K == 8192) {
-        if (a.M <= 4 || a.N >= 16384) return launch_parted<EPI>(a, s);
+        if (a.M <= 8 || a.N >= 16384) return launch_parted<EPI>(a, s);
         return launch_slice<EPI>(a, s);
     }
     // Specialised K: the GPT-2 widths.
