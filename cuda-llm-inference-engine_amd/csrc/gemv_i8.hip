@@ -842,7 +842,12 @@ void launch_burst(const GemmArgs& a, hipStream_t s) {
     constexpr int IPW = S <= 3 ? 8 : 2;  // 24 loads of weights per lane in flight
     const int items = (a.N + 3) / 4;
     const unsigned blocks = (unsigned)((items + 4 * IPW - 1) / (4 * IPW));
-    const bool nt = (size_t)a.N * (256 * S) >= kStreamWeightBytes;
+    // Non-temporal weight loads from 16 MiB up (the burst kernel takes N >=
+    // 16384): the 768 x 50257 LM head 8.87 -> 8.31 us with its weights
+    // rotated through 1 GiB, 3072 x 16390 10.8 -> 9.9 us, and the GPT-2 decode
+    // step with the INT8 LM head 225.9 -> 223.2 us (batch 1) and 336.4 ->
+    // 334.6 us (batch 16), where plain loads would leave the head in the MALL.
+    const bool nt = (size_t)a.N * (256 * S) >= ((size_t)16 << 20);
     auto go = [&](auto mb) {
         constexpr int MB = decltype(mb)::value;
         auto* k = nt ? gemv_i8_burst_kernel<EPI, true, MB, S, IPW> : gemv_i8_burst_kernel<EPI, false, MB, S, IPW>;
