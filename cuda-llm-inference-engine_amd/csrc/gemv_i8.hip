@@ -878,10 +878,15 @@ template <int MT, int EPI>
 void launch_mt(const GemmArgs& a, hipStream_t s) {
     // Wide GPT-2-width GEMVs (the 768 x 50257 LM head): all of a wave's
     // loads at once (M = 1 / 4 / 8: 0.49 / 0.44 / 0.39 -> 0.52 / 0.51 / 0.49
-    // of HBM peak per graph-replayed launch; level at M = 16, and slower on
-    // the narrow shapes, whose time is launch latency).
-    if (a.N >= 16384 && a.M <= 8) {
-        if (a.K == 768) return launch_burst<EPI, 3>(a, s);
+    // of HBM peak per graph-replayed launch; slower on the narrow shapes,
+    // whose time is launch latency).  At 9 <= M <= 16 it takes K = 3072
+    // (N = 16390, weights rotated through 1 GiB: 18.3 -> 13.5 us at M = 16
+    // against the MFMA GEMV); at K = 768 the MFMA GEMV stays, whose plain
+    // loads keep an LM head in the MALL between decode steps (GPT-2 batch-16
+    // step with the INT8 head 337.0 -> 334.6 us, although a standalone
+    // launch on rotated weights is 2% slower).
+    if (a.N >= 16384) {
+        if (a.K == 768 && a.M <= 8) return launch_burst<EPI, 3>(a, s);
         if (a.K == 3072) return launch_burst<EPI, 12>(a, s);
     }
     if constexpr (MT > 4) {

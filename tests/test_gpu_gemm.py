@@ -94,9 +94,10 @@ def test_i32_lm_head_shape(ie, orc, M):
 @pytest.mark.parametrize("M,N,K", [(9, 16390, 3072), (16, 16400, 3072), (12, 50257, 768), (16, 20001, 768)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
 def test_wide_n_mfma_gemv_epilogues(ie, orc, M, N, K, epi):
-    """The MFMA GEMV at 9 <= M <= 16 with a wide N (K = 768 / 3072): ragged
-    last 16-feature group, every epilogue; int32 and Plain/Bias/Residual
-    bit-exact, GELU to 2e-6."""
+    """9 <= M <= 16 with a wide N: the MFMA GEMV at K = 768 (ragged last
+    16-feature group), the burst GEMV's 16-row form at K = 3072 (ragged last
+    4-feature item); every epilogue; int32 and Plain/Bias/Residual bit-exact,
+    GELU to 2e-6."""
     A, W = problem(M, N, K, 17 * M + N + epi)
     r = rng(37 + epi)
     bias = (r.standard_normal(N) * 0.5).astype(np.float32)
