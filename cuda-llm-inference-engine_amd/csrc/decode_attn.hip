@@ -36,7 +36,11 @@
 // single split pass 1 writes O itself and pass 2 is skipped.  (A
 // "last split to arrive merges" variant needs a device-scope release per
 // workgroup, which on gfx950 writes back the XCD's L2 and cost more than the
-// second launch.)
+// second launch.  Without the release, partials written by agent-scope
+// atomic stores, a counter per (b, kv head) and the last workgroup merging
+// with agent-scope loads gave the same bits but took longer still: cfg3
+// 13.65 -> 16.5 us, since that workgroup's store, counter and load round
+// trips run one after another at the end of the launch.)
 #include <algorithm>
 #include <cmath>
 #include <map>
