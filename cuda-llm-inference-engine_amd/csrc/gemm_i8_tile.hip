@@ -9,8 +9,8 @@
 // small workgroups per CU cover it better than one large one.  The tile is
 // BM x BN (64 x 64 or 128 x 64) on four waves (2 x 2, each (BM/2) x (BN/2)
 // as 32x32 blocks of v_mfma_i32_32x32x32_i8), and K advances through a ring
-// of NSTAGE 128-byte stages in LDS (2-3, or 4 for long K), NSTAGE - 1 of them
-// in flight while one is read:
+// of NSTAGE 128-byte stages in LDS (2-3; 4 for long K or a one-round grid),
+// NSTAGE - 1 of them in flight while one is read:
 //   * global -> LDS copies are global_load_lds_dwordx4 (16 B per lane straight
 //     into LDS); a wave-load fills 8 rows x 128 B; the lane -> global address
 //     map applies the LDS swizzle, so the lane-ordered destination lands each
@@ -247,15 +247,20 @@ struct TileLaunch {
     // than L2 (GPT-2 prefill TTFT at batch 1: 0.705 -> 0.684 ms; weights
     // rotated through 1 GiB, M = 512, N = 768: 7.55 -> 5.95 us; the same
     // weights every launch, L2-resident: 5.09 -> 5.20 us), and four over long
-    // K (K = 3072); a whole-K ring (six stages, one workgroup per CU) lost
-    // wherever there are more tiles than CUs; 128 x 128 tiles lost everywhere.
+    // K (K = 3072) or when the grid is one round of workgroups, one per CU
+    // (rotated weights, K = 768: M = 512, N = 768 5.88 -> 5.37 us; M = 128,
+    // N = 2304 6.01 -> 5.41 us, N = 3072 6.05 -> 5.49 us; with 288-384 tiles
+    // four stages measured 3% slower); six or eight stages measured slower
+    // still, in one round too (K = 3072: 10.4 -> 10.9-11.1 us); 128 x 128
+    // tiles lost everywhere.
     static void run(const GemmArgs& a, hipStream_t s) {
         const bool long_k = a.K >= 2048;
         if (gemm_i8_tile_shape(a) == 128064) {
             if (long_k) go<128, 64, 4>(a, s);
             else go<128, 64, 2>(a, s);
         } else {
-            if (long_k) go<64, 64, 4>(a, s);
+            const long long tiles = (long long)((a.M + 63) / 64) * ((a.N + 63) / 64);
+            if (long_k || tiles <= num_cus()) go<64, 64, 4>(a, s);
             else go<64, 64, 3>(a, s);
         }
     }

@@ -274,14 +274,17 @@ def test_prefill_sized_wide_gemm(ie, orc, M, N, K, epi):
         assert np.array_equal(got, want), np.abs(got - want).max()
 
 
-@pytest.mark.parametrize("M,N,K", [(600, 1100, 128), (600, 1000, 384), (700, 900, 640)])
+@pytest.mark.parametrize("M,N,K", [(1100, 1000, 128), (1100, 1000, 384), (1200, 1100, 640),
+                                   (600, 1100, 128), (600, 1000, 256), (600, 1000, 384), (700, 900, 640)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
 def test_tile_kernel_short_k_ring(ie, orc, M, N, K, epi):
-    """The 64x64 LDS tile kernel's three-stage ring against K stage counts
-    below, equal to and past the ring: one 128-byte stage (the prologue and
-    the loop re-read it into the other slots), three, and five (the ring
-    wraps: the last stage sits in slot 1); ragged M and N, the whole output, int32 and
-    Plain/Bias/Residual bit-exact, GELU to 2e-6."""
+    """The 64x64 LDS tile kernel's short-K rings: three stages when the grid
+    takes more than one round of workgroups (1100x1000: 288 tiles, 1200x1100:
+    342, on 256 CUs) and four when it fits one (600x1100: 180 tiles, 165-160),
+    against K stage counts below, equal to and past the ring: one 128-byte
+    stage (the prologue and the loop re-read it into the other slots), two,
+    three, and five (the ring wraps); ragged M and N, the whole output, int32
+    and Plain/Bias/Residual bit-exact, GELU to 2e-6."""
     A, W = problem(M, N, K, 13 * M + N + K + epi)
     r = rng(29 + epi)
     bias = (r.standard_normal(N) * 0.5).astype(np.float32)
