@@ -171,16 +171,17 @@ void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s) {
         launch_gemm_i8_big(a, s);
         return;
     }
-    // Prefill-sized problems: the multi-stage LDS tile kernel (M = 2048:
-    // 22.1 -> 12.1 us at N = 2304, 37.7 -> 13.0 us at K = 3072, N = 768;
-    // at par with or ahead of hipBLASLt on the same shapes); below 64 tiles,
-    // register streaming.
-    if (gemm_i8_tile_applies(a)) {
-        launch_gemm_i8_tile(a, s);
-        return;
-    }
+    // Small grids (one round of 32 x 32 blocks): the K-split kernel that
+    // streams each block's K through per-wave LDS rings.
     if (gemm_i8_stream_applies(a)) {
         launch_gemm_i8_stream(a, s);
+        return;
+    }
+    // Prefill-sized problems: the multi-stage LDS tile kernel (M = 2048:
+    // 22.1 -> 12.1 us at N = 2304, 37.7 -> 13.0 us at K = 3072, N = 768;
+    // at par with or ahead of hipBLASLt on the same shapes).
+    if (gemm_i8_tile_applies(a)) {
+        launch_gemm_i8_tile(a, s);
         return;
     }
     dispatch_epilogue<MfmaLaunch>(a.epi, a, s);

@@ -1,5 +1,6 @@
 // gemm_i8_tile.hip — INT8 GEMM for prefill-sized problems on gfx950 (M of a
-// few hundred to a few thousand rows, GPT-2-sized N and K).
+// few hundred to a few thousand rows, GPT-2-sized N and K, more 32 x 32
+// blocks than two per CU).
 //
 // Result identical to the reference's K14 kernel (kernels/quantization/
 // 14_int8_gemm.cu:65-170): exact int32 K-sum, then the dequant epilogue.
@@ -275,14 +276,13 @@ int gemm_i8_tile_shape(const GemmArgs& a) {
     return t >= 2LL * num_cus() ? 128064 : 64064;
 }
 
-// At fewer than 64 tiles of 64 x 64 (M = 128, N = 768: 24) the
-// register-streamed kernel, which splits K over waves, is faster (4.2 against
-// 4.9 us; K = 3072: 8.2 against 9.8 us).
+// Grids small enough for one round of 32 x 32 blocks take the K-split
+// stream kernel first (gemm_i8_stream_applies).
 bool gemm_i8_tile_applies(const GemmArgs& a) {
     if (a.K % BK != 0 || a.K == 0) return false;
     if (((uintptr_t)a.A % 16) || ((uintptr_t)a.BT % 16)) return false;
     const long long t = (long long)((a.M + 63) / 64) * ((a.N + 63) / 64);
-    return t >= 64 && t < (1LL << 31);
+    return t < (1LL << 31);
 }
 
 void launch_gemm_i8_tile(const GemmArgs& a, hipStream_t s) {

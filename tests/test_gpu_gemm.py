@@ -220,15 +220,19 @@ def test_epilogues(ie, orc, M, K, N, path, epi):
 
 
 @pytest.mark.parametrize("M,N,K", [(100, 300, 128), (33, 65, 384), (520, 4100, 256), (1000, 2100, 768),
-                                   (128, 768, 3072), (97, 700, 640), (130, 770, 2048)])
+                                   (128, 768, 3072), (97, 700, 640), (130, 770, 2048), (1, 100, 256),
+                                   (31, 33, 1024), (40, 200, 8192)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
-def test_register_streamed_kernel(ie, orc, M, N, K, epi):
+def test_small_grid_stream_kernel(ie, orc, M, N, K, epi):
     """Mid-size shapes (K % 128 == 0, too few 256x256 tiles for the large-tile
-    kernel): below 64 tiles of 64x64 the register-streamed MFMA kernel, with K
-    split over 4 waves (128x768x3072, 130x770x2048) and 2 waves (97x700x640);
-    above, the 64x64 LDS tile kernel (520x4100x256, 1000x2100x768).  Ragged M
-    and N, every epilogue; int32 and Plain/Bias/Residual bit-exact, GELU to
-    2e-6."""
+    kernel): while the 32x32 blocks of C fit two per CU (512 on 256 CUs) the
+    kernel whose two waves split a block's K and stream it through their own
+    LDS rings (one K-group each at
+    100x300x128, so the second wave's range is empty; one row, 1x100x256;
+    128x768x3072, 130x770x2048, 97x700x640, 33x65x384, 31x33x1024 and
+    40x200x8192, 32 groups per wave, past the ring); beyond, the 64x64
+    LDS tile kernel (520x4100x256, 1000x2100x768).  Ragged M and N, every
+    epilogue; int32 and Plain/Bias/Residual bit-exact, GELU to 2e-6."""
     A, W = problem(M, N, K, 7 * M + N + K + epi)
     r = rng(11 + epi)
     bias = (r.standard_normal(N) * 0.5).astype(np.float32)
