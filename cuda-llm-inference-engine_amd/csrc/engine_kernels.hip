@@ -9,8 +9,12 @@
 // Positions and token ids live in device memory, so a captured decode step
 // replays without host involvement.  prefill_qkv_write does the same split and
 // append for a prompt chunk (P tokens per sequence, src/gpt2_engine.cu:466-
-// 481 with seq_len = P).
+// 481 with seq_len = P).  ln_quant is prefill's LayerNorm and per-row
+// quantizer in one launch.
+#include <stdexcept>
+
 #include "device_util.h"
+#include "gemv_common.h"
 #include "ie_internal.h"
 
 namespace ie {
@@ -62,6 +66,27 @@ __global__ __launch_bounds__(256) void prefill_qkv_write_kernel(
     Q[idx] = row[i];
     kc[slot * d + i] = to_kv<KV>(row[d + i]);
     vc[slot * d + i] = to_kv<KV>(row[2 * d + i]);
+}
+
+// Prefill's LayerNorm (src/gpt2_engine.cu:455) and the per-row quantizer
+// of the GEMM input after it (:460) in one launch: one wave per row, the
+// row's float4s loaded once, normalised and quantized in registers
+// (stage_row: the LayerNorm's and then the quantizer's arithmetic, so the
+// bytes and scale equal those of ie_layernorm followed by
+// ie_quantize_fp32_to_int8), and the fp32 LayerNorm output never written.
+template <int K>
+__global__ __launch_bounds__(256) void ln_quant_kernel(int rows, const float* __restrict__ x,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta, float eps,
+                                                       int32_t* __restrict__ q, float* __restrict__ scales) {
+    const int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (row >= rows) return;  // whole waves
+    GemvFusion f;
+    f.gamma = gamma;
+    f.beta = beta;
+    f.eps = eps;
+    stage_row<K, kSrcLnQuant>(x + (size_t)row * K, f, q + (size_t)row * (K / 4), scales + row,
+                              (int)(threadIdx.x & 63));
 }
 
 // The fp32 comparison backend's epilogue after a vendor fp32 GEMM g [M, N]
@@ -128,6 +153,15 @@ void launch_prefill_qkv_write(int B, int P, int start, int d, const float* qkv,
         prefill_qkv_write_kernel<float><<<blocks, 256, 0, s>>>(
             B, P, start, d, qkv, block_table, nbps, block_size, Q, static_cast<float*>(kc),
             static_cast<float*>(vc));
+}
+
+bool ln_quant_supported(int cols) { return cols == 768; }
+
+void launch_ln_quant(int rows, int cols, const float* x, const float* gamma, const float* beta, float eps,
+                     int32_t* q, float* scales, hipStream_t s) {
+    if (rows == 0) return;
+    if (cols != 768) throw std::logic_error("launch_ln_quant: no kernel for this width");
+    ln_quant_kernel<768><<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(rows, x, gamma, beta, eps, q, scales);
 }
 
 void launch_fp32_epilogue(int M, int N, const float* g, const float* bias, const float* residual, float* out,

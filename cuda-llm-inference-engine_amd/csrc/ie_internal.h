@@ -174,6 +174,12 @@ void launch_prefill_qkv_write(int B, int P, int start, int d, const float* qkv,
                               void* kc, void* vc, int kv_dtype, hipStream_t s);
 // positions[b] = ctx_lens[b] = pos for every sequence.
 void launch_set_positions(int B, int pos, int* positions, int* ctx_lens, hipStream_t s);
+// LayerNorm of rows x cols fp32 then the per-row int8 quantizer, in one
+// launch, the bytes and scales of ie_layernorm + ie_quantize_fp32_to_int8
+// (engine_kernels.hip); only for widths where ln_quant_supported.
+bool ln_quant_supported(int cols);
+void launch_ln_quant(int rows, int cols, const float* x, const float* gamma, const float* beta, float eps,
+                     int32_t* q, float* scales, hipStream_t s);
 // fp32 comparison backend: out = epilogue(g) for epi in {BIAS, BIAS_GELU,
 // BIAS_RESIDUAL}, g [M, N] the vendor GEMM's output (out may alias residual).
 void launch_fp32_epilogue(int M, int N, const float* g, const float* bias, const float* residual, float* out,

@@ -607,6 +607,23 @@ struct GPT2Engine::Impl {
         IEC(ie_int8_gemm(M, w.N, w.K, aq, w.packed, as, w.scale, epi, bias, res, out, st));
     }
 
+    // Prefill's LayerNorm-fed projection: LayerNorm of pf.x [M, K], the
+    // per-row quantizer, the INT8 GEMM.  With the INT8 backend at a width
+    // launch_ln_quant takes, the LayerNorm and the quantizer are one launch
+    // with the bytes of the pair; otherwise the C-ABI ops.
+    void ln_linear(int M, const float* gamma, const float* beta, const QuantWeight& w, const float* wf, int epi,
+                   const float* bias, float* out) {
+        ie_stream_t st = (ie_stream_t)stream;
+        if (!fp32 && ie::ln_quant_supported(w.K)) {
+            ie::launch_ln_quant(M, w.K, pf.x, gamma, beta, 1e-5f, pf.act_q, pf.act_s, stream);
+            IEC(ie::check_launch("ln_quant"));
+            IEC(ie_int8_gemm(M, w.N, w.K, pf.act_q, w.packed, pf.act_s, w.scale, epi, bias, nullptr, out, st));
+            return;
+        }
+        IEC(ie_layernorm(M, w.K, pf.x, gamma, beta, pf.xn, 1e-5f, st));
+        linear(M, w, wf, pf.xn, epi, bias, nullptr, out, pf.act_q, pf.act_s, pf.gemm_out);
+    }
+
     void enqueue_step(int B) {
         if (fused)
             enqueue_step_fused(B);
@@ -801,7 +818,9 @@ struct GPT2Engine::Impl {
     // pos .. pos + P - 1, as M = B x chunk-row GEMMs and the causal prefill
     // attention over the paged cache, in chunks of prefill_chunk(B) tokens
     // per sequence (a later chunk attends to the earlier ones through the
-    // cache).  Every operation goes through the public C ABI.  Leaves the
+    // cache).  Every operation goes through the public C ABI but two: each
+    // LayerNorm and the quantizer of its output are one launch (same bytes,
+    // ln_linear), and the Q split + K/V append.  Leaves the
     // logits [B, V] of each sequence's last token, their argmax in `tokens`,
     // and positions at pos + P.  The reference prefills only a fresh session
     // and feeds a continuation through decode steps; here both prefill.
@@ -827,9 +846,7 @@ struct GPT2Engine::Impl {
                 IEC(ie_embedding(pf.ids + (size_t)b * Pc, Pc, pos, d, wte, wpe, pf.x + (size_t)b * Pc * d, st));
             for (int l = 0; l < cfg.n_layers; ++l) {
                 const Layer& L = layers[l];
-                IEC(ie_layernorm(M, d, pf.x, L.ln1_g, L.ln1_b, pf.xn, 1e-5f, st));
-                linear(M, L.qkv, L.qkv_f, pf.xn, IE_EPI_BIAS, L.qkv_b, nullptr, pf.qkv, pf.act_q, pf.act_s,
-                       pf.gemm_out);
+                ln_linear(M, L.ln1_g, L.ln1_b, L.qkv, L.qkv_f, IE_EPI_BIAS, L.qkv_b, pf.qkv);
                 ie::launch_prefill_qkv_write(B, Pc, pos, d, pf.qkv, block_table, nbps, kBlock, pf.q, layer_k(l),
                                              layer_v(l), opt.kv_dtype, stream);
                 IEC(ie::check_launch("prefill_qkv_write"));
@@ -837,9 +854,7 @@ struct GPT2Engine::Impl {
                                     kBlock, pos, pf.attn, st));
                 linear(M, L.out, L.out_f, pf.attn, IE_EPI_BIAS_RESIDUAL, L.out_b, pf.x, pf.x, pf.act_q, pf.act_s,
                        pf.gemm_out);
-                IEC(ie_layernorm(M, d, pf.x, L.ln2_g, L.ln2_b, pf.xn, 1e-5f, st));
-                linear(M, L.up, L.up_f, pf.xn, IE_EPI_BIAS_GELU, L.up_b, nullptr, pf.h, pf.act_q, pf.act_s,
-                       pf.gemm_out);
+                ln_linear(M, L.ln2_g, L.ln2_b, L.up, L.up_f, IE_EPI_BIAS_GELU, L.up_b, pf.h);
                 linear(M, L.down, L.down_f, pf.h, IE_EPI_BIAS_RESIDUAL, L.down_b, pf.x, pf.x, pf.act_q, pf.act_s,
                        pf.gemm_out);
             }
