@@ -68,6 +68,18 @@ __global__ __launch_bounds__(256) void prefill_qkv_write_kernel(
     vc[slot * d + i] = to_kv<KV>(row[2 * d + i]);
 }
 
+// The cache slot of every row of a prompt chunk (the addressing of
+// prefill_qkv_write), for the QKV GEMM that stores K/V itself.
+__global__ __launch_bounds__(256) void prefill_row_slots_kernel(int B, int P, int start,
+                                                                const int* __restrict__ block_table, int nbps,
+                                                                int block_size, int* __restrict__ row_slot) {
+    const int m = blockIdx.x * 256 + threadIdx.x;
+    if (m >= B * P) return;
+    const int b = m / P, pos = start + (m - b * P);
+    const int blk = pos / block_size;
+    row_slot[m] = block_table[(size_t)b * nbps + blk] * block_size + (pos - blk * block_size);
+}
+
 // Prefill's LayerNorm (src/gpt2_engine.cu:455) and the per-row quantizer
 // of the GEMM input after it (:460) in one launch: one wave per row, the
 // row's float4s loaded once, normalised and quantized in registers
@@ -153,6 +165,14 @@ void launch_prefill_qkv_write(int B, int P, int start, int d, const float* qkv,
         prefill_qkv_write_kernel<float><<<blocks, 256, 0, s>>>(
             B, P, start, d, qkv, block_table, nbps, block_size, Q, static_cast<float*>(kc),
             static_cast<float*>(vc));
+}
+
+void launch_prefill_row_slots(int B, int P, int start, const int* block_table, int nbps, int block_size,
+                              int* row_slot, hipStream_t s) {
+    const int rows = B * P;
+    if (rows == 0) return;
+    prefill_row_slots_kernel<<<(rows + 255) / 256, 256, 0, s>>>(B, P, start, block_table, nbps, block_size,
+                                                                 row_slot);
 }
 
 bool ln_quant_supported(int cols) { return cols == 768; }

@@ -17,7 +17,9 @@
 
 #include <cstdint>
 
+#include "device_util.h"
 #include "ie_amd.h"
+#include "ie_internal.h"
 
 namespace ie {
 
@@ -72,6 +74,25 @@ __device__ __forceinline__ void store_epilogue(void* C, size_t idx, int32_t acc,
         bias_v = bias[n];
     if constexpr (EPI == IE_EPI_BIAS_RESIDUAL) res_v = residual[idx];
     store_epilogue_v<EPI, NT>(C, idx, acc, sa, sb, bias_v, res_v);
+}
+
+// kEpiQKVRoute: one routed store of the bias epilogue's value for row m,
+// column n, the row's cache slot given (row_slot[m], gathered before the
+// stores like the other epilogue operands).
+__device__ __forceinline__ void route_store(const QkvRoute& r, int m, int n, int slot, int32_t acc, float sa,
+                                            float sb, float bias_v) {
+    const float v = epilogue_value<IE_EPI_BIAS>(acc, sa, sb, bias_v, 0.0f);
+    if (n < r.d) {
+        r.q[(size_t)m * r.d + n] = v;
+        return;
+    }
+    const bool is_k = n < 2 * r.d;
+    const size_t i = (size_t)slot * r.d + (is_k ? n - r.d : n - 2 * r.d);
+    void* base = is_k ? r.kc : r.vc;
+    if (r.kv_dtype == IE_KV_BF16)
+        static_cast<uint16_t*>(base)[i] = f32_to_bf16_rne(v);
+    else
+        static_cast<float*>(base)[i] = v;
 }
 
 // Runtime-to-compile-time epilogue dispatch.

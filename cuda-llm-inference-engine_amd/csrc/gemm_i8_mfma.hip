@@ -19,6 +19,8 @@
 // same lane, so the product is the full K-sum whatever order the hardware
 // adds them in.  Accumulator v of lane l holds C[8*(v/4) + 4*(l/32) + v%4]
 // [l % 32] of the 32x32 block.
+#include <stdexcept>
+
 #include "device_util.h"
 #include "epilogue.h"
 #include "ie_internal.h"
@@ -155,6 +157,16 @@ struct MfmaLaunch {
 };
 
 }  // namespace
+
+void launch_gemm_i8_qkv_route(const GemmArgs& a, hipStream_t s) {
+    if (a.M == 0 || a.N == 0) return;
+    if (gemm_i8_stream_applies(a))
+        launch_gemm_i8_stream(a, s);
+    else if (gemm_i8_tile_applies(a))
+        launch_gemm_i8_tile(a, s);
+    else
+        throw std::logic_error("launch_gemm_i8_qkv_route: K % 128 != 0 or unaligned operands");
+}
 
 void launch_gemm_i8_mfma(const GemmArgs& a, hipStream_t s) {
     if (a.M == 0 || a.N == 0) return;

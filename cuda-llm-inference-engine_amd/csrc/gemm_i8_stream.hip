@@ -72,7 +72,7 @@ template <int EPI, int KS>
 __global__ __launch_bounds__(64 * KS) void gemm_i8_stream_kernel(
     int M, int N, int K, const int8_t* __restrict__ A, const int8_t* __restrict__ BT,
     const float* __restrict__ sA, const float* __restrict__ sB, const float* bias,
-    const float* residual, void* C) {
+    const float* residual, void* C, const QkvRoute route) {
     static_assert((KS - 1) * 64 * (int)sizeof(i32x16) <= KS * LR * LSLOT, "partial tiles fit the rings");
     __shared__ __attribute__((aligned(1024))) int8_t lds[KS * LR * LSLOT];
     const int lane = threadIdx.x & 63;
@@ -140,9 +140,12 @@ __global__ __launch_bounds__(64 * KS) void gemm_i8_stream_kernel(
     // stores (vmcnt counts stores, and C may alias them).
     const int cbase = n0 + (lane & 31);
     const int rbase = m0 + 4 * (lane >> 5);
-    constexpr bool HAS_BIAS = EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL;
+    constexpr bool ROUTE = EPI == kEpiQKVRoute;
+    constexpr bool HAS_BIAS =
+        EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL || ROUTE;
     constexpr bool HAS_RES = EPI == IE_EPI_BIAS_RESIDUAL;
     float sa[16] = {}, sb = 0.0f, bv = 0.0f, rv[16] = {};
+    int slot[ROUTE ? 16 : 1] = {};
     if constexpr (EPI != IE_EPI_I32) {
         const int n = min(cbase, N - 1);
         sb = sB[n];
@@ -152,6 +155,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_i8_stream_kernel(
             const int m = min(rbase + 8 * (v >> 2) + (v & 3), M - 1);
             sa[v] = sA[m];
             if constexpr (HAS_RES) rv[v] = residual[(size_t)m * N + n];
+            if constexpr (ROUTE) slot[v] = route.row_slot[m];
         }
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -165,7 +169,11 @@ __global__ __launch_bounds__(64 * KS) void gemm_i8_stream_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int m = rbase + 8 * (v >> 2) + (v & 3);
-            if (m < M) store_epilogue_v<EPI>(C, (size_t)m * N + cbase, acc[v], sa[v], sb, bv, rv[v]);
+            if (m >= M) continue;
+            if constexpr (ROUTE)
+                route_store(route, m, cbase, slot[v], acc[v], sa[v], sb, bv);
+            else
+                store_epilogue_v<EPI>(C, (size_t)m * N + cbase, acc[v], sa[v], sb, bv, rv[v]);
         }
     }
 }
@@ -177,7 +185,7 @@ struct StreamLaunch {
         const dim3 grid((a.N + 31) / 32, (a.M + 31) / 32);
         gemm_i8_stream_kernel<EPI, KS><<<grid, 64 * KS, 0, s>>>(
             a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A), reinterpret_cast<const int8_t*>(a.BT),
-            a.sA, a.sB, a.bias, a.residual, a.C);
+            a.sA, a.sB, a.bias, a.residual, a.C, a.route);
     }
     static void run(const GemmArgs& a, hipStream_t s) {
         if (a.K / KG >= 2)
@@ -204,7 +212,10 @@ bool gemm_i8_stream_applies(const GemmArgs& a) {
 
 void launch_gemm_i8_stream(const GemmArgs& a, hipStream_t s) {
     if (a.M == 0 || a.N == 0) return;
-    dispatch_epilogue<StreamLaunch>(a.epi, a, s);
+    if (a.epi == kEpiQKVRoute)
+        StreamLaunch<kEpiQKVRoute>::run(a, s);
+    else
+        dispatch_epilogue<StreamLaunch>(a.epi, a, s);
 }
 
 }  // namespace ie

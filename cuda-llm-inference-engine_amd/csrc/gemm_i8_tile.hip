@@ -62,13 +62,17 @@ __global__ __launch_bounds__(256) void gemm_i8_tile_kernel(int M, int N, int K, 
                                                            const float* __restrict__ sA,
                                                            const float* __restrict__ sB, const float* bias,
                                                            const float* residual, void* C, int tiles_m,
-                                                           int tiles_n) {
+                                                           int tiles_n, const QkvRoute route) {
     constexpr int OA = BM * BK, STAGE = (BM + BN) * BK;
     constexpr int MI = BM / 64, NJ = BN / 64;  // 32x32 blocks per wave
     constexpr int LA = BM / 32, LB = BN / 32;  // wave-loads per operand per stage (8 rows each, 4 waves)
     constexpr int LPS = LA + LB;
     static_assert(MI >= 1 && NJ >= 1 && (NSTAGE - 1) * LPS <= 63, "tile and ring fit");
-    __shared__ __attribute__((aligned(1024))) int8_t lds[NSTAGE * STAGE];
+    // (kEpiQKVRoute: BM row slots after the ring, in the same array: a
+    // second LDS object would make the compiler drain the copies in flight
+    // before every LDS read of the K loop)
+    constexpr bool ROUTE = EPI == kEpiQKVRoute;
+    __shared__ __attribute__((aligned(1024))) int8_t lds[NSTAGE * STAGE + (ROUTE ? BM * 4 : 0)];
 
     // XCD-aware, grouped tile order.
     const int nwg = gridDim.x;
@@ -172,10 +176,18 @@ __global__ __launch_bounds__(256) void gemm_i8_tile_kernel(int M, int N, int K, 
     const int h = lane >> 5;
     const int rbase = m0 + wm * (BM / 2) + 4 * h;
     const int cbase = n0 + wn * (BN / 2) + (lane & 31);
-    constexpr bool HAS_BIAS = EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL;
+    constexpr bool HAS_BIAS =
+        EPI == IE_EPI_BIAS || EPI == IE_EPI_BIAS_GELU || EPI == IE_EPI_BIAS_RESIDUAL || ROUTE;
     constexpr bool HAS_RES = EPI == IE_EPI_BIAS_RESIDUAL;
     auto row = [&](int i, int v) { return rbase + i * 32 + 8 * (v >> 2) + (v & 3); };
     float sa[MI][16] = {}, sb[NJ] = {}, bv[NJ] = {}, rv[MI][16][NJ] = {};
+    // kEpiQKVRoute: the tile's row slots go to LDS (32 of them per lane in
+    // registers cost a wave per SIMD), read back beside each store
+    int* lslot = reinterpret_cast<int*>(lds + NSTAGE * STAGE);
+    if constexpr (ROUTE) {
+        if (threadIdx.x < BM) lslot[threadIdx.x] = route.row_slot[min(m0 + (int)threadIdx.x, M - 1)];
+        __syncthreads();
+    }
     if constexpr (EPI != IE_EPI_I32) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
@@ -219,7 +231,10 @@ __global__ __launch_bounds__(256) void gemm_i8_tile_kernel(int M, int N, int K, 
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const int n = cbase + j * 32;
-                if (n < N)
+                if (n >= N) continue;
+                if constexpr (ROUTE)
+                    route_store(route, m, n, lslot[m - m0], acc[i][j][v], sa[i][v], sb[j], bv[j]);
+                else
                     store_epilogue_v<EPI, NT>(C, (size_t)m * N + n, acc[i][j][v], sa[i][v], sb[j], bv[j], rv[i][v][j]);
             }
         }
@@ -234,10 +249,13 @@ struct TileLaunch {
         // C of 16 MiB or more goes out with non-temporal stores (M = 2048:
         // N = 2304 12.5 -> 10.9 us, N = 3072 13.5 -> 11.0 us; at N = 768,
         // 6.3 MB of C, they measured slower: 6.15 -> 6.7 us)
-        auto* k = (size_t)a.M * a.N * 4 >= ((size_t)16 << 20) ? gemm_i8_tile_kernel<EPI, BM, BN, NSTAGE, true>
-                                                            : gemm_i8_tile_kernel<EPI, BM, BN, NSTAGE, false>;
+        // (routed stores are plain: Q and the caches are read next)
+        auto* k = gemm_i8_tile_kernel<EPI, BM, BN, NSTAGE, false>;
+        if constexpr (EPI != kEpiQKVRoute)
+            if ((size_t)a.M * a.N * 4 >= ((size_t)16 << 20)) k = gemm_i8_tile_kernel<EPI, BM, BN, NSTAGE, true>;
         k<<<tm * tn, 256, 0, s>>>(a.M, a.N, a.K, reinterpret_cast<const int8_t*>(a.A),
-                                 reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C, tm, tn);
+                                 reinterpret_cast<const int8_t*>(a.BT), a.sA, a.sB, a.bias, a.residual, a.C, tm, tn,
+                                 a.route);
     }
     // Measured on the GPT-2 prefill shapes (M = 128-2048, K = 768 / 3072,
     // N = 768-3072, bias epilogue; same box, bit-identical C): 128 x 64 tiles
@@ -287,7 +305,10 @@ bool gemm_i8_tile_applies(const GemmArgs& a) {
 
 void launch_gemm_i8_tile(const GemmArgs& a, hipStream_t s) {
     if (a.M == 0 || a.N == 0) return;
-    dispatch_epilogue<TileLaunch>(a.epi, a, s);
+    if (a.epi == kEpiQKVRoute)
+        TileLaunch<kEpiQKVRoute>::run(a, s);
+    else
+        dispatch_epilogue<TileLaunch>(a.epi, a, s);
 }
 
 }  // namespace ie

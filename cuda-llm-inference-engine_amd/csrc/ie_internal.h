@@ -21,6 +21,22 @@ void launch_quantize(int rows, int cols, const float* in, int32_t* packed,
                      float* scales, hipStream_t s);
 
 // ---- INT8 GEMM ----
+// Where a prefill QKV projection's outputs go when the GEMM stores them
+// itself (launch_gemm_i8_qkv_route), as prefill_qkv_write moves them: output
+// column n < d of row m goes to q[m * d + n], column d + i (2d + i) to
+// element i of the K (V) cache row of slot row_slot[m] (bf16 rounded to
+// nearest even when kv_dtype is IE_KV_BF16).  row_slot comes from
+// launch_prefill_row_slots, once per prompt chunk (every layer's cache has
+// the same slots).
+struct QkvRoute {
+    float* q = nullptr;
+    void* kc = nullptr;
+    void* vc = nullptr;
+    int kv_dtype = IE_KV_F32;
+    const int* row_slot = nullptr;
+    int d = 0;
+};
+
 struct GemmArgs {
     int M, N, K;
     const int32_t* A;
@@ -31,7 +47,14 @@ struct GemmArgs {
     const float* residual;
     void* C;
     int epi;
+    QkvRoute route{};  // epi == kEpiQKVRoute only
 };
+// The bias epilogue with the output routed by GemmArgs::route (C unused).
+constexpr int kEpiQKVRoute = 9;
+// The prefill QKV projection: the bias-epilogue INT8 GEMM [M, 3d] on the
+// small-grid or tile kernel, as launch_gemm_i8_mfma would choose, its
+// outputs stored by a.route (gemm_i8_mfma.hip).
+void launch_gemm_i8_qkv_route(const GemmArgs& a, hipStream_t s);
 // dot4 GEMV for small M (gemv_i8.hip); M in [1, 16].
 void launch_gemv_i8(const GemmArgs& a, hipStream_t s);
 
@@ -178,6 +201,11 @@ void launch_set_positions(int B, int pos, int* positions, int* ctx_lens, hipStre
 // launch, the bytes and scales of ie_layernorm + ie_quantize_fp32_to_int8
 // (engine_kernels.hip); only for widths where ln_quant_supported.
 bool ln_quant_supported(int cols);
+// row_slot[m] for the rows m = b * P + t of a prompt chunk (token t of
+// sequence b at position start + t): its cache slot table[b * nbps + pos /
+// block_size] * block_size + pos % block_size (engine_kernels.hip).
+void launch_prefill_row_slots(int B, int P, int start, const int* block_table, int nbps, int block_size,
+                              int* row_slot, hipStream_t s);
 void launch_ln_quant(int rows, int cols, const float* x, const float* gamma, const float* beta, float eps,
                      int32_t* q, float* scales, hipStream_t s);
 // fp32 comparison backend: out = epilogue(g) for epi in {BIAS, BIAS_GELU,

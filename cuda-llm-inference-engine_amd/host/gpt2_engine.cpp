@@ -320,6 +320,7 @@ struct GPT2Engine::Impl {
         float* gemm_out = nullptr;  // fp32 backend
         int* ids = nullptr;  // pinned host mirror in host_ids
         int* host_ids = nullptr;
+        int* row_slot = nullptr;  // cache slot of each row of the chunk (prefill_qkv)
     } pf;
     std::vector<void*> pf_allocs;
 
@@ -624,6 +625,38 @@ struct GPT2Engine::Impl {
         linear(M, w, wf, pf.xn, epi, bias, nullptr, out, pf.act_q, pf.act_s, pf.gemm_out);
     }
 
+    // Prefill's first LayerNorm, QKV projection and Q split + K/V append for
+    // B x Pc rows at positions pos ..: with the INT8 backend at a width
+    // launch_ln_quant takes, two launches (the LayerNorm + quantizer, then
+    // the GEMM storing Q and the K/V rows itself, where prefill_qkv_write
+    // would move them from pf.qkv); otherwise ln_linear into pf.qkv and
+    // prefill_qkv_write.
+    bool qkv_routed() const { return !fp32 && ie::ln_quant_supported(cfg.d_model); }
+
+    void prefill_qkv(int B, int Pc, int l) {
+        const Layer& L = layers[l];
+        const int d = cfg.d_model, M = B * Pc;
+        if (qkv_routed()) {  // pf.row_slot holds this chunk's slots
+            ie::launch_ln_quant(M, d, pf.x, L.ln1_g, L.ln1_b, 1e-5f, pf.act_q, pf.act_s, stream);
+            IEC(ie::check_launch("ln_quant"));
+            ie::GemmArgs a{M, L.qkv.N, L.qkv.K, pf.act_q, L.qkv.packed, pf.act_s, L.qkv.scale, L.qkv_b,
+                           nullptr, nullptr, ie::kEpiQKVRoute};
+            a.route.q = pf.q;
+            a.route.kc = layer_k(l);
+            a.route.vc = layer_v(l);
+            a.route.kv_dtype = opt.kv_dtype;
+            a.route.row_slot = pf.row_slot;
+            a.route.d = d;
+            ie::launch_gemm_i8_qkv_route(a, stream);
+            IEC(ie::check_launch("qkv_route"));
+            return;
+        }
+        ln_linear(M, L.ln1_g, L.ln1_b, L.qkv, L.qkv_f, IE_EPI_BIAS, L.qkv_b, pf.qkv);
+        ie::launch_prefill_qkv_write(B, Pc, pos, d, pf.qkv, block_table, nbps, kBlock, pf.q, layer_k(l),
+                                     layer_v(l), opt.kv_dtype, stream);
+        IEC(ie::check_launch("prefill_qkv_write"));
+    }
+
     void enqueue_step(int B) {
         if (fused)
             enqueue_step_fused(B);
@@ -808,6 +841,7 @@ struct GPT2Engine::Impl {
         pf.act_s = static_cast<float*>(alloc(R * 4));
         if (fp32) pf.gemm_out = static_cast<float*>(alloc(R * std::max(3 * d, ff) * 4));
         pf.ids = static_cast<int*>(alloc(R * 4));
+        pf.row_slot = static_cast<int*>(alloc(R * 4));
         HIPC(hipHostMalloc(&pf.host_ids, R * sizeof(int)));
         pf.rows = rows;
     }
@@ -818,9 +852,10 @@ struct GPT2Engine::Impl {
     // pos .. pos + P - 1, as M = B x chunk-row GEMMs and the causal prefill
     // attention over the paged cache, in chunks of prefill_chunk(B) tokens
     // per sequence (a later chunk attends to the earlier ones through the
-    // cache).  Every operation goes through the public C ABI but two: each
+    // cache).  Every operation goes through the public C ABI but these: each
     // LayerNorm and the quantizer of its output are one launch (same bytes,
-    // ln_linear), and the Q split + K/V append.  Leaves the
+    // ln_linear), and the Q split + K/V append is the QKV GEMM's epilogue
+    // (prefill_qkv) or its own launch.  Leaves the
     // logits [B, V] of each sequence's last token, their argmax in `tokens`,
     // and positions at pos + P.  The reference prefills only a fresh session
     // and feeds a continuation through decode steps; here both prefill.
@@ -844,12 +879,13 @@ struct GPT2Engine::Impl {
             HIPC(hipMemcpyAsync(pf.ids, pf.host_ids, sizeof(int) * M, hipMemcpyHostToDevice, stream));
             for (int b = 0; b < B; ++b)
                 IEC(ie_embedding(pf.ids + (size_t)b * Pc, Pc, pos, d, wte, wpe, pf.x + (size_t)b * Pc * d, st));
+            if (qkv_routed()) {
+                ie::launch_prefill_row_slots(B, Pc, pos, block_table, nbps, kBlock, pf.row_slot, stream);
+                IEC(ie::check_launch("prefill_row_slots"));
+            }
             for (int l = 0; l < cfg.n_layers; ++l) {
                 const Layer& L = layers[l];
-                ln_linear(M, L.ln1_g, L.ln1_b, L.qkv, L.qkv_f, IE_EPI_BIAS, L.qkv_b, pf.qkv);
-                ie::launch_prefill_qkv_write(B, Pc, pos, d, pf.qkv, block_table, nbps, kBlock, pf.q, layer_k(l),
-                                             layer_v(l), opt.kv_dtype, stream);
-                IEC(ie::check_launch("prefill_qkv_write"));
+                prefill_qkv(B, Pc, l);
                 IEC(ie_prefill_attn(B, Pc, H, H, dh, pf.q, layer_k(l), layer_v(l), opt.kv_dtype, block_table, nbps,
                                     kBlock, pos, pf.attn, st));
                 linear(M, L.out, L.out_f, pf.attn, IE_EPI_BIAS_RESIDUAL, L.out_b, pf.x, pf.x, pf.act_q, pf.act_s,
