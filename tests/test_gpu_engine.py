@@ -300,6 +300,31 @@ def test_prefill_bf16_kv_and_int8_head(ie, mid_dir):
         check_steps(seq)
 
 
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+def test_prefill_batch16_rows_equal_single_prompts(ie, mid_dir, kv):
+    """768-wide model, 16 prompts of 40 tokens: the batch's prefill GEMMs run
+    on the 64x64 / 128x64 tile kernels (M = 640; the QKV projection storing Q
+    and the fp32 or bf16 K/V rows through its routed epilogue, slots in LDS),
+    a single prompt's on the small-grid K-split kernel (M = 40).  Both give
+    exact int32 sums and the same per-element epilogue, and attention, the
+    LayerNorms and the head work per sequence, so each sequence's prefill
+    logits, and the decode steps over the cache its prefill wrote, are
+    bit-identical either way."""
+    kw = dict(kv_dtype=ie.KV_BF16) if kv == "bf16" else {}
+    rng = np.random.default_rng(90)
+    prompts = rng.integers(0, 1000, (16, 40)).astype(np.int32)
+    toks = rng.integers(0, 1000, (3, 16)).astype(np.int32)
+    eng = ie.Engine(mid_dir, max_batch=16, **kw)
+    batch = [eng.prefill(prompts)] + [eng.step(toks[i]) for i in range(3)]
+    eng.close()
+    for b in (0, 7, 15):
+        one = ie.Engine(mid_dir, max_batch=1, **kw)
+        single = [one.prefill(prompts[b:b + 1])] + [one.step(toks[i, b:b + 1]) for i in range(3)]
+        one.close()
+        for i, (got, want) in enumerate(zip(single, batch)):
+            assert np.array_equal(got[0], want[b]), (kv, b, i, np.abs(got[0] - want[b]).max())
+
+
 def test_prefill_chunking_and_batch_invariance_bit_exact(ie, mid_dir):
     """Every prefill row is computed independently of the others: GEMM rows
     are exact int32 sums with a per-row epilogue, and a query's attention
