@@ -39,7 +39,13 @@ def problem(M, N, K, seed):
 
 
 # ------------------------------------------------------------------ quantizer
-@pytest.mark.parametrize("rows,cols", [(1, 768), (16, 3072), (4, 8192), (130, 516), (3, 4), (256, 768)])
+# Widths on both sides of each form's limit (one wave per row up to 1024
+# columns, 256 threads with the row in registers up to 4096, two passes
+# beyond), row counts not a multiple of the four rows per workgroup, and the
+# batch-16 prefill sizes.
+@pytest.mark.parametrize("rows,cols", [(1, 768), (16, 3072), (4, 8192), (130, 516), (3, 4), (256, 768),
+                                       (5, 256), (7, 260), (9, 1024), (6, 1028), (3, 2048), (5, 4096),
+                                       (3, 4100), (2048, 768), (2048, 3072)])
 def test_quantize_bit_exact(ie, orc, rows, cols):
     r = rng(rows * 31 + cols)
     x = (r.standard_normal((rows, cols)) * r.uniform(1e-3, 1e3, (rows, 1))).astype(np.float32)
