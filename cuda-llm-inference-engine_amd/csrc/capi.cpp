@@ -220,7 +220,8 @@ int ie_prefill_attn(int B, int P, int H_q, int H_kv, int d, const float* Q, cons
     if (!Q || !O || !k_cache || !v_cache || !block_table) return fail(IE_ERR_INVALID, "prefill_attn: null pointer");
     if (!aligned(Q, 16) || !aligned(O, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
         return fail(IE_ERR_INVALID, "prefill_attn: Q, O and the caches must be 16-byte aligned");
-    if (B > 65535 || H_q > 65535) return fail(IE_ERR_UNSUPPORTED, "prefill_attn: grid too large");
+    if ((long long)((P + 15) / 16) * H_q * B > 0x7fffffffLL)
+        return fail(IE_ERR_UNSUPPORTED, "prefill_attn: grid too large (ceil(P/16) x H_q x B > 2^31 - 1)");
     ie::PrefillArgs a{};
     a.B = B; a.P = P; a.H_q = H_q; a.H_kv = H_kv; a.d = d;
     a.Q = Q; a.k = k_cache; a.v = v_cache; a.kv_dtype = kv_dtype;
@@ -240,7 +241,8 @@ int ie_flash_attn(int B, int H, int N, int d, const float* Q, const float* K, co
     if (!Q || !K || !V || !O) return fail(IE_ERR_INVALID, "flash_attn: null pointer");
     if (!aligned(Q, 16) || !aligned(K, 16) || !aligned(V, 16) || !aligned(O, 16))
         return fail(IE_ERR_INVALID, "flash_attn: Q, K, V and O must be 16-byte aligned");
-    if (B > 65535 || H > 65535) return fail(IE_ERR_UNSUPPORTED, "flash_attn: grid too large");
+    if ((long long)((N + 15) / 16) * H * B > 0x7fffffffLL)
+        return fail(IE_ERR_UNSUPPORTED, "flash_attn: grid too large (ceil(N/16) x H x B > 2^31 - 1)");
     // O is written while other workgroups still read Q, K and V.
     const uintptr_t bytes = (uintptr_t)B * H * N * d * sizeof(float);
     const uintptr_t o0 = (uintptr_t)O, o1 = o0 + bytes;

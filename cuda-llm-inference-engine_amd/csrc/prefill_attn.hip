@@ -14,11 +14,18 @@
 //   * contiguous [B, H, N, d] fp32 for Q, K, V, O (the reference's K10
 //     signature, run_flash_attn_v2).
 //
-// MI355X layout (grid = query tiles x H_q x B, four waves per workgroup):
+// MI355X layout (one workgroup of four waves per (query tile, h, b)):
 //   * a workgroup owns 16 consecutive queries of one (b, h); its four waves
 //     take the 16-token KV chunks up to the tile's causal limit round-robin,
 //     each keeping its own running (m, l, o), and merge them in LDS at the end;
-//     tiles are dispatched longest first (they are causal triangles);
+//   * the grid is one-dimensional, tile rank major: workgroup u takes pair
+//     p = u % (H_q B) and tile rank r = u / (H_q B) (rank 0 = the last,
+//     longest tile), so the longest tiles (causal triangles) are dispatched
+//     first.  Workgroups go to the XCDs round-robin, so with H_q B a multiple
+//     of 8 all tiles of one (b, h) run on one XCD (its K/V fetched into one
+//     L2) and every XCD gets the same mix of tile lengths.  (With the tile
+//     index fastest, XCD x took tile rank x of every pair: at 8 tiles XCD 0
+//     held all the longest tiles, and each pair's K/V went to eight L2s);
 //   * S^T = K Q^T and O^T += V^T P^T run on v_mfma_f32_16x16x4_f32.  Lane l
 //     (i = l % 16, g = l / 16) holds, for query i of the tile:
 //       - q: elements d/4*g .. d/4*g + d/4 - 1 (the B operand: MFMA step s
@@ -173,8 +180,10 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i = lane & 15, g = lane >> 4;
     const int ntiles = (P + kQTile - 1) / kQTile;
-    const int qt = ntiles - 1 - (int)blockIdx.x;  // longest (last) tiles first
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int pairs = (int)(gridDim.x / (unsigned)ntiles);  // H_q B
+    const int r = (int)blockIdx.x / pairs, pr = (int)blockIdx.x - r * pairs;
+    const int qt = ntiles - 1 - r;  // longest (last) tiles first
+    const int h = pr % H_q, b = pr / H_q;
     const int kvh = h / (H_q / H_kv);
     const int q0 = qt * kQTile;
     const int qlast = min(q0 + kQTile - 1, P - 1);
@@ -289,7 +298,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(
 
 template <int D, typename KV, int LAYOUT, bool BS16>
 void launch_t(const PrefillArgs& a, hipStream_t s) {
-    const dim3 grid((a.P + kQTile - 1) / kQTile, a.H_q, a.B);
+    const dim3 grid((unsigned)((a.P + kQTile - 1) / kQTile * a.H_q * a.B));
     const float qscale = 1.4426950408889634f / sqrtf((float)D);
     prefill_attn_kernel<D, KV, LAYOUT, BS16><<<grid, 256, 0, s>>>(
         a.Q, static_cast<const KV*>(a.k), static_cast<const KV*>(a.v), a.block_table,

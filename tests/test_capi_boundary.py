@@ -137,7 +137,11 @@ def test_prefill_attn_validation(ie):
     assert prefill(ie, O=ctypes.c_void_p((1 << 20) + 8)) == ie.IE_ERR_INVALID
     assert prefill(ie, P=0) == ie.IE_OK
     assert prefill(ie, B=0) == ie.IE_OK
+    # one workgroup per (16-query tile, head, sequence) in a 1-D grid: 2^31 of them is one too many
+    assert prefill(ie, B=2048, P=16384, H_q=1024, H_kv=1, d=64, nbps=2048) == ie.IE_ERR_UNSUPPORTED
+    assert "grid too large" in ie.last_error()
     fa = lambda *a: st(ie, "ie_flash_attn", *a, None)  # noqa: E731
+    assert fa(2048, 1024, 16384, 64, FAKE, FAKE, FAKE, FAKE, 1) == ie.IE_ERR_UNSUPPORTED
     assert fa(1, 2, 64, 96, FAKE, FAKE, FAKE, FAKE, 1) == ie.IE_ERR_UNSUPPORTED
     assert fa(1, 2, 64, 64, FAKE, None, FAKE, FAKE, 1) == ie.IE_ERR_INVALID
     assert fa(1, 2, -1, 64, FAKE, FAKE, FAKE, FAKE, 1) == ie.IE_ERR_INVALID

@@ -77,10 +77,13 @@ def test_prefill_other_block_sizes(ie, orc, bs):
     assert rel_err(got, want) < REL
 
 
-def test_prefill_gpt2_prompt(ie, orc):
-    """The BASELINE prompt shape: 128 tokens, 12 heads of 64, batch 4."""
-    B, P, H, d = 4, 128, 12, 64
-    Q, kc, vc, table = case(300, B, P, 0, H, 1, d, 16, 0)
+@pytest.mark.parametrize("B", [4, 16])
+def test_prefill_gpt2_prompt(ie, orc, B):
+    """The BASELINE prompt shape: 128 tokens, 12 heads of 64, batch 4 and the
+    engine's batch 16 (192 (sequence, head) pairs: every tile of a pair on one
+    XCD)."""
+    P, H, d = 128, 12, 64
+    Q, kc, vc, table = case(300 + B, B, P, 0, H, 1, d, 16, 0)
     want = oracle_prefill(orc, Q, kc, vc, table, 0, 16, H)
     got = host(ie.prefill_attn(dev(Q), dev(kc), dev(vc), dev(table), 0, 16, H))
     assert rel_err(got, want) < REL
