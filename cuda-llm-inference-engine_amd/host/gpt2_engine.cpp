@@ -305,9 +305,8 @@ struct GPT2Engine::Impl {
     // copied), and ring_ev[slot] marks their arrival.
     int* host_ring = nullptr;
     hipEvent_t ring_ev[2] = {nullptr, nullptr};
-    // top-k sampler: k values then k indices in one device buffer
-    // [2 kTopkMax words] and its pinned host copy (one transfer per token)
-    float* topk_buf = nullptr;
+    // top-k sampler: k values then k indices, written by the kernel into
+    // pinned host memory
     float* host_topk_buf = nullptr;
 
     // Prefill scratch [rows, ...], rows = sequences x chunk tokens, grown on
@@ -435,12 +434,11 @@ struct GPT2Engine::Impl {
         HIPC(hipHostMalloc(&host_tokens, sizeof(int) * B));
         HIPC(hipHostMalloc(&host_ring, sizeof(int) * 2 * B, hipHostMallocCoherent));
         for (auto& e : ring_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-        topk_buf = dev<float>(2 * ie::kTopkMax);
         head_keys = dev<unsigned long long>(B);
         HIPC(hipMemset(head_keys, 0, sizeof(unsigned long long) * B));
         head_done = dev<unsigned>(1);
         HIPC(hipMemset(head_done, 0, sizeof(unsigned)));
-        HIPC(hipHostMalloc(&host_topk_buf, sizeof(float) * 2 * ie::kTopkMax));
+        HIPC(hipHostMalloc(&host_topk_buf, sizeof(float) * 2 * ie::kTopkMax, hipHostMallocCoherent));
         reset();
     }
 
@@ -799,13 +797,16 @@ struct GPT2Engine::Impl {
     };
 
     // Upload one token per sequence, run a step, fetch the argmax ids.
-    void step_tokens(const int* toks, int B, bool fetch) {
+    // sync = false leaves the step in flight: the caller must synchronize the
+    // stream before host_tokens is written again (the sampled loop's pick()
+    // does, right after queueing the top-k behind the step).
+    void step_tokens(const int* toks, int B, bool fetch, bool sync = true) {
         check_ids(toks, B);
         std::memcpy(host_tokens, toks, sizeof(int) * B);
         HIPC(hipMemcpyAsync(tokens, host_tokens, sizeof(int) * B, hipMemcpyHostToDevice, stream));
         run_step(B);
         if (fetch) HIPC(hipMemcpyAsync(host_tokens, tokens, sizeof(int) * B, hipMemcpyDeviceToHost, stream));
-        HIPC(hipStreamSynchronize(stream));
+        if (sync) HIPC(hipStreamSynchronize(stream));
     }
 
     // ---- prefill ----
@@ -1002,14 +1003,15 @@ void GPT2Engine::step(const int* tokens, int batch) {
 // reference's own route, the whole row to the host, with the same order for
 // equal values (lower index first) and the same draw.
 static int sample_top_k_engine(const float* d_logits, int V, int k, float temperature, unsigned seed,
-                               float* d_buf, float* h_buf, hipStream_t s) {
+                               float* h_buf, hipStream_t s) {
     k = std::max(1, std::min(k, V));
     int token = 0;
     if (k <= ie::kTopkMax) {
-        // values in words [0, k), indices in [k, 2k): one copy back
-        if (ie_topk(1, d_logits, V, k, d_buf, reinterpret_cast<int*>(d_buf + k), s) != IE_OK)
+        // The kernel writes values in words [0, k) and indices in [k, 2k)
+        // straight into the pinned host buffer (no copy behind it); the
+        // stream's completion makes them visible to the host.
+        if (ie_topk(1, d_logits, V, k, h_buf, reinterpret_cast<int*>(h_buf + k), s) != IE_OK)
             throw std::runtime_error(ie_last_error());
-        HIPC(hipMemcpyAsync(h_buf, d_buf, sizeof(float) * 2 * k, hipMemcpyDeviceToHost, s));
         HIPC(hipStreamSynchronize(s));
         if (ie_top_k_draw(h_buf, reinterpret_cast<const int*>(h_buf + k), k, temperature, seed, &token) != IE_OK)
             throw std::runtime_error(ie_last_error());
@@ -1047,8 +1049,8 @@ void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tok
         if (greedy) return I.host_tokens[0];
         const unsigned seed = first_pick ? 42u : ++sample_seed;
         first_pick = false;
-        return sample_top_k_engine(I.logits, I.cfg.vocab_size, top_k, temperature, seed, I.topk_buf,
-                                   I.host_topk_buf, I.stream);
+        return sample_top_k_engine(I.logits, I.cfg.vocab_size, top_k, temperature, seed, I.host_topk_buf,
+                                   I.stream);
     };
 
     const auto t_total = Clock::now();
@@ -1089,7 +1091,7 @@ void GPT2Engine::generate(const std::vector<int>& prompt_tokens, int max_new_tok
             metrics.tokens_generated = stepi + 1;
             if (I.pos >= I.cfg.max_seq_len) break;
             const auto t = Clock::now();
-            I.step_tokens(&next, 1, greedy);
+            I.step_tokens(&next, 1, greedy, false);  // pick() synchronizes behind the top-k
             next = pick();
             const float dt = ms_since(t);
             itl.push_back(dt);

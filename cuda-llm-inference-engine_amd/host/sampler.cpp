@@ -61,20 +61,19 @@ int draw(const float* vals, const int* idx, int k, float temperature, float r) {
     return idx[k - 1];
 }
 
-// Device and pinned host buffers of the compat samplers, made by ie_init()
+// The pinned, coherent host buffer of the compat samplers, made by ie_init()
 // (or by a sampler's first call when ie_init was not called) and kept for the
-// process (the reference allocates a host vector per call).
-// k values then k indices in one buffer, so one transfer brings both back.
+// process (the reference allocates a host vector per call): the selection
+// kernels write k values then k indices (or the argmax index) straight into
+// it, so no copy follows them.
 struct CompatBufs {
     std::mutex mu;
-    float* d_buf = nullptr;  // [2 kTopkMax] words
-    float* h_buf = nullptr;  // pinned copy
+    float* h_buf = nullptr;  // [2 kTopkMax] words
     bool ready() {
-        if (!d_buf && hipMalloc(&d_buf, sizeof(float) * 2 * ie::kTopkMax) != hipSuccess) d_buf = nullptr;
-        if (d_buf && !h_buf &&
-            hipHostMalloc(&h_buf, sizeof(float) * 2 * ie::kTopkMax, hipHostMallocDefault) != hipSuccess)
+        if (!h_buf &&
+            hipHostMalloc(&h_buf, sizeof(float) * 2 * ie::kTopkMax, hipHostMallocCoherent) != hipSuccess)
             h_buf = nullptr;
-        return h_buf != nullptr;  // what did succeed is kept for the next try
+        return h_buf != nullptr;
     }
 };
 
@@ -116,13 +115,13 @@ int sample_argmax(const float* d_logits, int vocab_size) {
         ie::fail(IE_ERR_HIP, "sample_argmax: buffer allocation failed");
         return -1;
     }
-    int* d_idx = reinterpret_cast<int*>(b.d_buf);
-    if (ie_argmax(1, d_logits, vocab_size, d_idx, nullptr) != IE_OK) return -1;
-    if (hipMemcpy(b.h_buf, d_idx, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) {
-        ie::fail(IE_ERR_HIP, "sample_argmax: copy failed");
+    int* h_idx = reinterpret_cast<int*>(b.h_buf);
+    if (ie_argmax(1, d_logits, vocab_size, h_idx, nullptr) != IE_OK) return -1;
+    if (hipStreamSynchronize(nullptr) != hipSuccess) {
+        ie::fail(IE_ERR_HIP, "sample_argmax: synchronize failed");
         return -1;
     }
-    return reinterpret_cast<const int*>(b.h_buf)[0];
+    return h_idx[0];
 }
 
 // src/sampler.cu:16-45: k clamped to the vocabulary as there; the selection
@@ -135,10 +134,10 @@ int sample_top_k(const float* d_logits, int vocab_size, int k, float temperature
         ie::fail(IE_ERR_HIP, "sample_top_k: buffer allocation failed");
         return -1;
     }
-    if (ie_topk(1, d_logits, vocab_size, k, b.d_buf, reinterpret_cast<int*>(b.d_buf + k), nullptr) != IE_OK)
+    if (ie_topk(1, d_logits, vocab_size, k, b.h_buf, reinterpret_cast<int*>(b.h_buf + k), nullptr) != IE_OK)
         return -1;
-    if (hipMemcpy(b.h_buf, b.d_buf, sizeof(float) * 2 * k, hipMemcpyDeviceToHost) != hipSuccess) {
-        ie::fail(IE_ERR_HIP, "sample_top_k: copy failed");
+    if (hipStreamSynchronize(nullptr) != hipSuccess) {
+        ie::fail(IE_ERR_HIP, "sample_top_k: synchronize failed");
         return -1;
     }
     int token = -1;
