@@ -243,9 +243,14 @@ void launch_argmax(int rows, const float* logits, int n, int* out,
 
 // ---- top-k sampler (sampler.hip, host/sampler.cpp) ----
 constexpr int kTopkMax = 1024;  // largest k selected on the device
-// Makes the device and pinned buffers of sample_argmax / sample_top_k
-// (called by ie_init, so the compat samplers allocate nothing afterwards).
+// Makes the pinned buffer of sample_argmax / sample_top_k (called by
+// ie_init, so the compat samplers allocate nothing afterwards).
 int compat_sampler_init();
+// k above kTopkMax: the reference's own route (src/sampler.cu:18-26), the
+// whole row to the host and a partial sort, equal values in index order,
+// then the reference's draw; IE_OK or an error code (message set).
+int host_top_k_token(const float* d_logits, int V, int k, float temperature, unsigned seed, hipStream_t s,
+                     int* token);
 void launch_topk(int rows, const float* logits, int n, int k, float* out_vals,
                  int* out_idx, hipStream_t s);
 

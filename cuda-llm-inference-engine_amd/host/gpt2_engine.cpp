@@ -1017,16 +1017,7 @@ static int sample_top_k_engine(const float* d_logits, int V, int k, float temper
             throw std::runtime_error(ie_last_error());
         return token;
     }
-    std::vector<float> h(V);
-    HIPC(hipMemcpyAsync(h.data(), d_logits, sizeof(float) * V, hipMemcpyDeviceToHost, s));
-    HIPC(hipStreamSynchronize(s));
-    std::vector<int> idx(V);
-    std::iota(idx.begin(), idx.end(), 0);
-    std::partial_sort(idx.begin(), idx.begin() + k, idx.end(),
-                      [&](int a, int b) { return h[a] > h[b] || (h[a] == h[b] && a < b); });
-    std::vector<float> vals(k);
-    for (int i = 0; i < k; ++i) vals[i] = h[idx[i]];
-    if (ie_top_k_draw(vals.data(), idx.data(), k, temperature, seed, &token) != IE_OK)
+    if (ie::host_top_k_token(d_logits, V, k, temperature, seed, s, &token) != IE_OK)
         throw std::runtime_error(ie_last_error());
     return token;
 }

@@ -6,9 +6,11 @@
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <mutex>
+#include <numeric>
 #include <vector>
 
 #include "../csrc/ie_internal.h"
@@ -85,6 +87,21 @@ CompatBufs& compat_bufs() {
 }  // namespace
 
 namespace ie {
+int host_top_k_token(const float* d_logits, int V, int k, float temperature, unsigned seed, hipStream_t s,
+                     int* token) {
+    std::vector<float> h(V);
+    if (hipMemcpyAsync(h.data(), d_logits, sizeof(float) * V, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return fail(IE_ERR_HIP, "top_k: logits copy failed");
+    std::vector<int> idx(V);
+    std::iota(idx.begin(), idx.end(), 0);
+    std::partial_sort(idx.begin(), idx.begin() + k, idx.end(),
+                      [&](int a, int b) { return h[a] > h[b] || (h[a] == h[b] && a < b); });
+    std::vector<float> vals(k);
+    for (int i = 0; i < k; ++i) vals[i] = h[idx[i]];
+    return ie_top_k_draw(vals.data(), idx.data(), k, temperature, seed, token);
+}
+
 int compat_sampler_init() {
     CompatBufs& b = compat_bufs();
     std::lock_guard<std::mutex> lock(b.mu);
@@ -128,6 +145,15 @@ int sample_argmax(const float* d_logits, int vocab_size) {
 // on the device (k up to IE_TOPK_MAX), the draw on the host.
 int sample_top_k(const float* d_logits, int vocab_size, int k, float temperature, unsigned int seed) {
     if (k > vocab_size) k = vocab_size;
+    if (k > ie::kTopkMax) {
+        int token = -1;
+        if (!d_logits || vocab_size <= 0) {
+            ie::fail(IE_ERR_INVALID, "sample_top_k: bad logits");
+            return -1;
+        }
+        return ie::host_top_k_token(d_logits, vocab_size, k, temperature, seed, nullptr, &token) == IE_OK ? token
+                                                                                                         : -1;
+    }
     CompatBufs& b = compat_bufs();
     std::lock_guard<std::mutex> lock(b.mu);
     if (!b.ready()) {

@@ -88,12 +88,13 @@ void run_embedding(const int* token_ids, int seq_len, int start_pos,
                    int d_model, const float* wte, const float* wpe, float* out);
 
 /* Samplers over device logits [vocab_size] (src/sampler.cu).  The argmax and
- * the top-k selection run on the device, so 4 bytes (argmax) or k value/index
- * pairs (top-k) come back instead of the whole row; k is clamped to
- * vocab_size as in the reference and must then be <= IE_TOPK_MAX.  The draw
- * follows the reference's float arithmetic and its srand(seed) / rand() rule
- * with a generator private to the library (see ie_top_k_draw).  Their two
- * small buffers (device and pinned host) are made by ie_init(), or by the
+ * the top-k selection run on the device and write their 4 bytes (argmax) or
+ * k value/index pairs (top-k) straight into pinned host memory instead of the
+ * whole row coming back; k is clamped to vocab_size as in the reference, and
+ * k above IE_TOPK_MAX takes the reference's route (the whole row to the host,
+ * a partial sort).  The draw follows the reference's float arithmetic and its
+ * srand(seed) / rand() rule with a generator private to the library (see
+ * ie_top_k_draw).  Their small pinned buffer is made by ie_init(), or by the
  * first call when ie_init() was not called, and kept.  -1 on error. */
 int sample_argmax(const float* d_logits, int vocab_size);
 int sample_top_k(const float* d_logits, int vocab_size, int k,

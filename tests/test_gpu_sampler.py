@@ -117,6 +117,13 @@ def test_compat_samplers_match_oracle(ie, orc):
         got = top_k(ctypes.c_void_p(d.data_ptr()), V, k, T, seed)
         assert got == orc.sample_top_k(row, k, T, seed), case
         assert amax(ctypes.c_void_p(d.data_ptr()), V) == orc.argmax(row)
+    # k above the device limit: the whole row to the host, as the reference
+    for case, (V, k) in enumerate([(50257, 2000), (3001, 3001), (1500, 5000)]):
+        row = (r.standard_normal(V) * 2).astype(np.float32)
+        d = torch.from_numpy(row).cuda()
+        seed = 100 + case
+        got = top_k(ctypes.c_void_p(d.data_ptr()), V, k, 1.3, seed)
+        assert got == orc.sample_top_k(row, min(k, V), 1.3, seed), (V, k)
 
 
 def test_engine_sampled_generation_matches_oracle_sampler(ie, orc):
