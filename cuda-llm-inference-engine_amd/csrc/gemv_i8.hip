@@ -864,13 +864,16 @@ void launch_burst(const GemmArgs& a, hipStream_t s) {
 // share the few hundred KB of weights and each wave's dot and epilogue chain
 // is shorter (GPT-2 Small batch-1 decode step 272 -> 252 us; 64 rows per
 // 4-wave workgroup before; one-wave workgroups for the 768 x 768 attention
-// output projection: 247.5 -> 246.5 us).
+// output projection: 247.5 -> 246.5 us).  M = 2 / 3-4: one group of 4 rows
+// per wave as well, on the MT waves that stage the activation rows (8 / 16
+// rows per workgroup; 64 before: batch 2 / 3 / 4 decode step 272 / 304 /
+// 309 -> 253 / 279 / 282 us, same bits).
 template <int EPI, int K, int SRC>
 void launch_fused(const GemmArgs& a, const GemvFusion& f, hipStream_t s) {
     if (a.M <= 1 && (K == 3072 || a.N <= 1024)) launch_fixed<1, EPI, K / 16, SRC, 1, 1>(a, s, f);
     else if (a.M <= 1) launch_fixed<1, EPI, K / 16, SRC, 1, 4>(a, s, f);
-    else if (a.M <= 2) launch_fixed<2, EPI, K / 16, SRC>(a, s, f);
-    else if (a.M <= 4) launch_fixed<4, EPI, K / 16, SRC>(a, s, f);
+    else if (a.M <= 2) launch_fixed<2, EPI, K / 16, SRC, 1, 2>(a, s, f);
+    else if (a.M <= 4) launch_fixed<4, EPI, K / 16, SRC, 1, 4>(a, s, f);
     else launch_mfma16<EPI, K / 64, SRC>(a, s, f);
 }
 

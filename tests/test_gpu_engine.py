@@ -187,7 +187,7 @@ def test_gpt2_width_bf16_kv_and_int8_head(ie, mid_dir):
     check_vs_oracle(ie, mid_dir, 5, 20, 6, dict(int8_lm_head=True), dict(int8_lm_head=True))
 
 
-@pytest.mark.parametrize("B", [1, 3, 6, 16])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 6, 16])
 def test_fused_step_bit_identical_to_unfused_step(ie, mid_dir, B):
     """The fused kernels (LayerNorm/quantizer prologues, QKV append epilogue)
     against the step built from the public C ABI
