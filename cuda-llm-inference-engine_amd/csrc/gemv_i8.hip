@@ -909,10 +909,17 @@ void launch_mt(const GemmArgs& a, hipStream_t s) {
         if (a.M <= 8 || a.N >= 16384) return launch_parted<EPI>(a, s);
         return launch_slice<EPI>(a, s);
     }
-    // Specialised K: the GPT-2 widths.
+    // Specialised K: the GPT-2 widths, with the decode step's grouping (one
+    // 4-row group per wave; one-wave workgroups at N <= 1024 and at K = 3072
+    // for M <= 2): M = 1 / 2 / 4 at 768 x 2304 3.83 / 3.92 / 4.17 -> 2.82 /
+    // 2.87 / 2.97 us, 3072 x 768 3.48 / 3.80 -> 3.01 / 3.63 us (M = 4 keeps
+    // four waves, level at 4.42 us), same bits; the step built from the C ABI
+    // 466 -> 451 us at batch 1, 546 -> 497 us at batch 4.
     if constexpr (MT <= 4) {
-        if (a.K == 768) return launch_fixed<MT, EPI, 48>(a, s);
-        if (a.K == 3072) return launch_fixed<MT, EPI, 192>(a, s);
+        if (a.K == 768 && a.N <= 1024) return launch_fixed<MT, EPI, 48, kSrcInt8, 1, 1>(a, s);
+        if (a.K == 768) return launch_fixed<MT, EPI, 48, kSrcInt8, 1, 4>(a, s);
+        if (a.K == 3072 && MT <= 2) return launch_fixed<MT, EPI, 192, kSrcInt8, 1, 1>(a, s);
+        if (a.K == 3072) return launch_fixed<MT, EPI, 192, kSrcInt8, 1, 4>(a, s);
     }
     const dim3 grid((a.N + kRowsPerWG - 1) / kRowsPerWG);
     gemv_i8_kernel<MT, EPI><<<grid, 256, 0, s>>>(a.M, a.N, a.K, a.A, a.BT, a.sA, a.sB, a.bias,

@@ -83,6 +83,14 @@ def test_i32_gemv_exact(ie, orc, M, K, N):
     i32_case(ie, orc, M, N, K, ie.PATH_GEMV, M * 7 + N + K)
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("K,N", [(768, 13), (768, 1001), (768, 1030), (3072, 1001), (3072, 2050)])
+def test_i32_gemv_ragged_n(ie, orc, M, K, N):
+    """The dot4 GEMV's row groups (4 rows per wave, one- and four-wave
+    workgroups) with a partial last group and N on both sides of 1024."""
+    i32_case(ie, orc, M, N, K, ie.PATH_GEMV, M * 13 + N + K)
+
+
 @pytest.mark.parametrize("M", [1, 16, 17, 64, 130, 512])
 @pytest.mark.parametrize("K,N", GPT2_KN)
 def test_i32_mfma_exact(ie, orc, M, K, N):
