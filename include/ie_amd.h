@@ -78,8 +78,8 @@ typedef enum { IE_KV_F32 = 0, IE_KV_BF16 = 1 } ie_kv_dtype;
 
 const char* ie_last_error(void);
 int ie_version(void);
-/* Optional: checks that the current device is gfx950, makes the two small
- * buffers of the compat samplers (sample_argmax / sample_top_k in
+/* Optional: checks that the current device is gfx950, makes the small pinned
+ * host buffer of the compat samplers (sample_argmax / sample_top_k in
  * ie_compat.h), so nothing allocates afterwards, and looks up the current
  * device's address of ie_decode_attn_noalloc's scratch; calling it first also
  * keeps the HIP runtime's one-time start-up out of timed regions. */
